@@ -1,0 +1,238 @@
+"""Benchmark: Block-RVQ decode GEMV at Llama-3-8B shapes (configuration c3).
+
+A step is one decode token (M = 1 by default) through every compressed linear
+of a 32-layer Llama-3-8B stack: per layer q/k/v/o (4096 or 1024 x 4096),
+gate/up (14336 x 4096) and down (4096 x 14336), each a single-stage Block-RVQ
+layer with a 4096-entry fp16 codebook, 16-bit indices and an fp16 scale shared
+by 128-row groups, bf16 activations.  Weights are seeded random (synthetic,
+no checkpoint); all 224 linears live in HBM at once (1.76 GB of indices), so
+every step streams cold compressed bytes.  The step is captured in a HIP graph
+and replayed; the timed region is exactly --steps replays.
+
+Prints one JSON line (metric, value in tok/s, roofline of the dominant kernel
+measured live with HIP events, CPU baseline of the reference's per_group op
+sequence timed on this host's cores).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--m 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from wal2026_amd import PackedGroupedBlockRVQLinear, synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_stack(cfg: synth.Config, dev: torch.device, layers: int):
+    gen = synth.generator(0, dev)
+    stack = []
+    for _ in range(layers):
+        layer = {}
+        for name, n, k in cfg.shapes():
+            enc = synth.make_encoding(n, k, cfg, gen, dev)
+            layer[name] = PackedGroupedBlockRVQLinear(enc, matmul_strategy="hip_block_rvq").to(dev)
+        stack.append(layer)
+    return stack
+
+
+def linear_bytes(cfg: synth.Config, n: int, k: int) -> int:
+    """Algorithmic compressed bytes of one linear: ids + codebooks + scales."""
+    B = -(-k // cfg.block_size)
+    G = 1 if cfg.group_rows is None else -(-n // cfg.group_rows)
+    ib = torch.empty(0, dtype=cfg.ids_dtype()).element_size()
+    return cfg.num_stages * n * B * ib + G * cfg.num_stages * cfg.codebook_size * cfg.block_size * 2 + n * 2
+
+
+def time_kernel_family(stack, name, x, reps: int = 3) -> float:
+    """Average duration (us) of one launch of `name`, from a HIP event pair
+    around every launch, cycling through all layers so each launch reads
+    weights not touched by the previous ones."""
+    stream = torch.cuda.current_stream()
+    times = []
+    for _ in range(reps):
+        pairs = []
+        for layer in stack:
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            layer[name](x)
+            b.record(stream)
+            pairs.append((a, b))
+        torch.cuda.synchronize()
+        times.extend(a.elapsed_time(b) * 1000.0 for a, b in pairs)
+    return sum(times) / len(times)
+
+
+def cpu_baseline(cfg: synth.Config, budget_s: float = 20.0) -> dict:
+    """The reference's default per_group op sequence (oracle/ref_ops.py) on
+    this host's cores, over one layer's linears; tok/s extrapolated to the
+    whole stack."""
+    from oracle import ref_ops
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    gen = synth.generator(0)
+    layer = []
+    for name, n, k in cfg.shapes():
+        enc = synth.make_encoding(n, k, cfg, gen)
+        groups = [dict(stage_ids=list(g.stage_ids), codebooks=list(g.codebooks), row_scale=g.row_scale.to(torch.float16),
+                       in_features=k) for g in enc.groups]
+        x = synth.make_activation(cfg.m, k, cfg.x_dtype, gen)
+        layer.append((groups, enc.row_slices, n, x))
+
+    def one_layer():
+        for groups, slices, n, x in layer:
+            ref_ops.per_group_forward(x, groups, slices, n)
+
+    one_layer()  # warmup
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        one_layer()
+        reps += 1
+        if time.perf_counter() - t0 > budget_s / 2 or reps >= 3:
+            break
+    per_layer = (time.perf_counter() - t0) / reps
+    return {
+        "value": round(cfg.m / (per_layer * cfg.layers), 4),
+        "unit": "tok/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"1 of {cfg.layers} layers ({len(cfg.shapes())} linears, M={cfg.m}), per_group torch op sequence "
+                  f"(oracle/ref_ops.py), {reps} reps after 1 warmup; {per_layer * 1e3:.1f} ms/layer, tok/s "
+                  f"extrapolated to {cfg.layers} layers",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c5"])
+    ap.add_argument("--m", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU only (the path has no multi-GPU code); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+
+    cfg = synth.CONFIGS[args.config]
+    if args.m != cfg.m:
+        cfg = synth.Config(**{**cfg.__dict__, "m": args.m})
+    layers = args.layers or cfg.layers
+    dev = torch.device("cuda", 0)
+    log(f"building {layers} layers of {cfg.name} on {torch.cuda.get_device_name(dev)}")
+    stack = build_stack(cfg, dev, layers)
+    gen = synth.generator(1, dev)
+    xs = {k: synth.make_activation(cfg.m, k, cfg.x_dtype, gen, dev) for k in {k for _, _, k in cfg.shapes()}}
+
+    def step():
+        for layer in stack:
+            for name, _n, k in cfg.shapes():
+                layer[name](xs[k])
+
+    step()  # builds every layer's descriptor outside the graph
+    torch.cuda.synchronize()
+    log("capturing one step in a HIP graph")
+    graph = torch.cuda.CUDAGraph()
+    cap_stream = torch.cuda.Stream()
+    cap_stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap_stream):
+        step()
+    torch.cuda.current_stream().wait_stream(cap_stream)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} graph replays")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1000.0 / args.steps
+    tok_s = cfg.m * 1000.0 / ms_per_step
+    us_per_layer = ms_per_step * 1000.0 / layers
+
+    # dominant kernel: the largest linear's decode launch, timed per launch
+    dom_name, dom_n, dom_k = max(cfg.shapes(), key=lambda s: s[1] * s[2])
+    log(f"timing the dominant kernel ({dom_name}, {dom_n}x{dom_k}) per launch")
+    dom_us = time_kernel_family(stack, dom_name, xs[dom_k])
+    dom_bytes = linear_bytes(cfg, dom_n, dom_k)
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    per_linear = {}
+    for name, n, k in cfg.shapes():
+        us = time_kernel_family(stack, name, xs[k], reps=1)
+        per_linear[name] = {"us": round(us, 3), "GBps": round(linear_bytes(cfg, n, k) / (us * 1e-6) / 1e9, 1)}
+    layer_bytes = cfg.compressed_bytes_per_layer()
+
+    result = {
+        "metric": "RVQ-GEMV us/layer & %HBM roofline (M=1); decode tok/s at Llama-8B shapes",
+        "value": round(tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random Block-RVQ encodings and activations)",
+        "config": {
+            "workload": f"{cfg.name}: Llama-3-8B-shaped {layers}-layer stack of compressed linears, "
+                        f"S={cfg.num_stages}, K={cfg.codebook_size}, d={cfg.block_size}, "
+                        f"{str(cfg.ids_dtype()).replace('torch.', '')} ids, scale per {cfg.scale_rows} rows, "
+                        f"decode M={cfg.m}, one HIP graph per step",
+            "layers": layers,
+            "m": cfg.m,
+            "us_per_layer": round(us_per_layer, 3),
+            "compressed_bytes_per_layer": layer_bytes,
+            "step_hbm_fraction": round(layer_bytes * layers / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "per_linear": per_linear,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"rvq_decode_kernel ({dom_name} {dom_n}x{dom_k})",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "avg_launch_us": round(dom_us, 3),
+            "algorithmic_bytes_per_launch": dom_bytes,
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(cfg)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,189 @@
+/*
+ * wal2026_amd.h -- C ABI of the MI355X (gfx950) Block-RVQ / route-codebook
+ * linear library (libwal2026_amd.so).
+ *
+ * This is the drop-in boundary for the reference's DRL-runtime compressed
+ * linear forward.  The reference is pure Python (PyTorch + Triton); these entry
+ * points are what its Python layer binds (through ctypes)
+ * in place of the torch/Triton calls cited on each declaration.  Paths are
+ * relative to the reference repository root.
+ *
+ * Conventions
+ *  - Plain C types only: device pointers are `const void*`, the HIP stream is
+ *    passed as `void*` (a hipStream_t; NULL = the null stream).
+ *  - Every entry point returns WAL_OK (0) or a negative wal_status.  On error
+ *    wal_last_error() returns a message (thread-local).  Argument errors are
+ *    found on the host before any launch; launches are checked with
+ *    hipGetLastError().
+ *  - Nothing here allocates device memory or synchronises the stream.
+ *  - Tensors are dense and row-major.  Element types are given by wal_dtype
+ *    tags.
+ */
+#ifndef WAL2026_AMD_H
+#define WAL2026_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WAL_RVQ_MAX_STAGES 8
+#define WAL_ABI_VERSION 1
+
+typedef enum wal_dtype {
+  WAL_U8 = 0,   /* index planes, codebook_size <= 256 (src/block_vq.py:160-165) */
+  WAL_I16 = 1,  /* index planes, codebook_size <= 32767 */
+  WAL_U16 = 2,  /* index planes, codebook_size <= 65536 */
+  WAL_I32 = 3,  /* index planes, larger codebooks */
+  WAL_F16 = 10,
+  WAL_BF16 = 11,
+  WAL_F32 = 12
+} wal_dtype;
+
+typedef enum wal_status {
+  WAL_OK = 0,
+  WAL_EINVAL = -1,       /* bad argument (shape, dtype, null pointer) */
+  WAL_EUNSUPPORTED = -2, /* valid input this library does not handle */
+  WAL_EHIP = -3,         /* HIP runtime error (launch failure etc.) */
+  WAL_ESIZE = -4         /* caller buffer too small */
+} wal_status;
+
+/* Which of the reference's dequantisation semantics a call reproduces. */
+typedef enum wal_rvq_semantics {
+  /* PackedBlockRVQGroup.reconstruct_weight (src/runtime.py:379-414): fp32 sum
+   * of all stages, round to the output dtype, times row_scale rounded to it.
+   * Used by strategies per_group / full_weight / chunked_weight /
+   * stacked_matmul (src/runtime.py:1365-1370, :1501-1507). */
+  WAL_RVQ_RECONSTRUCT = 0,
+  /* PackedBlockRVQGroup.reconstruct_weight_fast (src/runtime.py:568-598):
+   * arithmetic in the output dtype over the active stages only.  Used by
+   * per_group_fast / full_weight_fast (:1371-1376, :1491-1500). */
+  WAL_RVQ_RECONSTRUCT_FAST = 1
+} wal_rvq_semantics;
+
+/* The buffers of one PackedBlockRVQGroup (src/runtime.py:249-290), device
+ * pointers.  The group produces output rows [row0, row0 + rows). */
+typedef struct wal_rvq_group {
+  const void* stage_ids[WAL_RVQ_MAX_STAGES]; /* [rows, blocks_per_row], id dtype */
+  const void* codebooks[WAL_RVQ_MAX_STAGES]; /* [codebook_size, block_size] */
+  const void* stage_scales;                  /* [num_stages] or NULL */
+  const void* row_scale;                     /* [ceil(rows / scale_rows)] */
+  const void* block_scale;                   /* [rows, blocks_per_row] or NULL */
+  int32_t row0;
+  int32_t rows;
+} wal_rvq_group;
+
+/* One PackedGroupedBlockRVQLinear (src/runtime.py:1175-1232): G groups that
+ * share the layer-wide constants below. */
+typedef struct wal_rvq_layer {
+  int32_t in_features;
+  int32_t out_features;
+  int32_t block_size;       /* d */
+  int32_t blocks_per_row;   /* B = padded_cols / d */
+  int32_t codebook_size;    /* K */
+  int32_t num_stages;       /* S, 1..WAL_RVQ_MAX_STAGES */
+  int32_t id_dtype;         /* WAL_U8 / WAL_I16 / WAL_U16 / WAL_I32 */
+  int32_t codebook_dtype;   /* WAL_F16 / WAL_BF16 / WAL_F32 */
+  int32_t scale_dtype;      /* row_scale, stage_scales and block_scale dtype */
+  int32_t scale_rows;       /* rows per row_scale entry; 1 = per row */
+  int32_t n_groups;
+  int32_t reserved;
+  const wal_rvq_group* groups;  /* host array [n_groups]; groups[g].row0 ascending, contiguous */
+  const void* plan;             /* device copy of the plan (see wal_rvq_plan_build),
+                                   required when n_groups > 1, else may be NULL */
+} wal_rvq_layer;
+
+/* ---- plan: device-side group and tile tables ---------------------------- */
+
+/* Bytes of the plan image for this layer.  No reference counterpart: the
+ * reference walks its groups in a Python loop (src/runtime.py:1502-1506);
+ * here one launch covers every group and reads them from this table. */
+int wal_rvq_plan_size(const wal_rvq_layer* layer, size_t* bytes);
+
+/* Write the plan image into host memory `dst` (`bytes` from
+ * wal_rvq_plan_size).  The caller copies it to device memory and stores the
+ * device pointer in layer->plan.  The image embeds the group device pointers,
+ * so it must be rebuilt if any buffer moves. */
+int wal_rvq_plan_build(const wal_rvq_layer* layer, void* dst, size_t bytes);
+
+/* ---- Block-RVQ entry points --------------------------------------------- */
+
+/* Dense weight [out_features, in_features] in out_dtype (F16/BF16/F32).
+ * Replaces PackedGroupedBlockRVQLinear.reconstruct_weight /
+ * reconstruct_weight_fast (src/runtime.py:1234-1240), i.e. the per-group
+ * PackedBlockRVQGroup.reconstruct_weight (src/runtime.py:379-414) or
+ * reconstruct_weight_fast (:568-598) concatenated on rows.  Bit-exact with
+ * the reference for every finite result.  active_stage_mask (FAST only): bit
+ * s set = stage s active (src/runtime.py:352-377); 0 means all stages. */
+int wal_rvq_reconstruct(const wal_rvq_layer* layer, int semantics,
+                        uint32_t active_stage_mask, void* w_out, int out_dtype,
+                        void* stream);
+
+/* y[m, n] = sum_k x[m, k] * W[n, k] + bias[n], W as wal_rvq_reconstruct would
+ * produce it in x_dtype, accumulated in fp32 and rounded once to y_dtype.
+ * Replaces PackedGroupedBlockRVQLinear.forward (src/runtime.py:1362-1507) for
+ * the dequantise-then-F.linear strategies.  x [m, in_features] F16/BF16, y
+ * [m, out_features] F16/BF16/F32, bias [out_features] or NULL (its dtype is
+ * bias_dtype; the reference keeps a bf16 buffer, :1229-1230, and casts it to
+ * x.dtype, which this call reproduces).  m >= 1; m <= 16 runs the decode
+ * kernel, larger m the prefill kernel. */
+int wal_rvq_linear(const wal_rvq_layer* layer, int semantics,
+                   uint32_t active_stage_mask, const void* x, int64_t m,
+                   int x_dtype, const void* bias, int bias_dtype, void* y,
+                   int y_dtype, void* stream);
+
+/* The fused Triton kernel's arithmetic: per block the fp32 sum of all stages
+ * is cast to x_dtype, contracted in fp32, and the row scale is applied to the
+ * accumulator (not per weight).  Replaces rvq_group_linear_matmul
+ * (src/triton_id_matmul.py:220-306); unlike it, any block_size and U8/I16/
+ * U16/I32 ids are accepted.  stage_ids [S, n, blocks_per_row], codebooks
+ * [S, codebook_size, block_size] (F16/BF16, stage scales already folded as
+ * in src/runtime.py:867-873), row_scale [n], x [m, k_in], out [m, n]. */
+int wal_rvq_group_linear_matmul(const void* x, int64_t m, int64_t k_in, int x_dtype,
+                                const void* stage_ids, int id_dtype, int32_t num_stages,
+                                int64_t n, int64_t blocks_per_row,
+                                const void* codebooks, int cb_dtype, int64_t codebook_size,
+                                int32_t block_size, const void* row_scale, int rs_dtype,
+                                void* out, int out_dtype, void* stream);
+
+/* ---- scalar route codebook (d = 1) ---------------------------------------- */
+
+/* Route-codebook linear: y = x @ W^T (+ bias), W[n, k] = f(codebook_sum[ids[n, k]],
+ * row_scale[n]).  mode 0 reproduces PackedIDRouteLinear.forward
+ * (src/runtime.py:89-97: product in the buffers' dtype, then cast to x
+ * dtype; bias cast to x dtype before F.linear); mode 1 reproduces
+ * FusedIDRouteLinear.forward / id_route_linear_matmul
+ * (src/runtime.py:100-105, src/triton_id_matmul.py:55-62: each operand cast to
+ * x dtype, product in x dtype; bias added to the rounded output).
+ * ids [n, k] I16/U16/I32, codebook_sum [routes] and row_scale [n] F16/BF16
+ * (same dtype), bias [n] (bias_dtype) or NULL. */
+int wal_id_route_linear(const void* x, int64_t m, int64_t k, int x_dtype,
+                        const void* ids, int id_dtype, int64_t n,
+                        const void* codebook_sum, int64_t routes, int cs_dtype,
+                        const void* row_scale, const void* bias, int bias_dtype,
+                        int mode, void* y, int y_dtype, void* stream);
+
+/* Dense route-codebook weight [n, k] in out_dtype.  mode 0 reproduces
+ * PackedIDRouteLinear.reconstruct_weight (src/runtime.py:89-93: the product
+ * codebook_sum[id] * row_scale in the buffers' dtype), then the cast to
+ * out_dtype that forward applies (:97); mode 1 the per-weight value of
+ * id_route_linear_matmul (src/triton_id_matmul.py:59-60). */
+int wal_id_route_reconstruct(const void* ids, int id_dtype, int64_t n, int64_t k,
+                             const void* codebook_sum, int64_t routes, int cs_dtype,
+                             const void* row_scale, int mode, int out_dtype, void* w_out,
+                             void* stream);
+
+/* ---- misc ---------------------------------------------------------------- */
+
+/* Message for the last error on this thread ("" if none). */
+const char* wal_last_error(void);
+
+/* WAL_ABI_VERSION of the loaded library. */
+int wal_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WAL2026_AMD_H */

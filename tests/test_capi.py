@@ -1,0 +1,148 @@
+"""The C ABI on the CPU: the library loads, exports exactly what
+include/wal2026_amd.h declares, builds plans, and refuses malformed calls
+before any launch (no GPU is touched by these tests)."""
+from __future__ import annotations
+
+import ctypes
+import re
+import struct
+from pathlib import Path
+
+import pytest
+
+from wal2026_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "wal2026_amd.h"
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^(?:int|const char\s*\*)\s*(wal_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    assert L.wal_abi_version() == _lib.ABI_VERSION
+    assert L.wal_last_error() == b""
+
+
+def _fake_layer(rows_per_group, in_features=64, S=2, K=256, id_dtype=_lib.U8, block=8, plan=None):
+    groups = (_lib.WalGroup * len(rows_per_group))()
+    r0 = 0
+    for i, rows in enumerate(rows_per_group):
+        for s in range(S):
+            groups[i].stage_ids[s] = 0x100000 + 0x1000 * i + s * 16
+            groups[i].codebooks[s] = 0x200000 + 0x1000 * i + s * 16
+        groups[i].row_scale = 0x300000 + 0x1000 * i
+        groups[i].row0 = r0
+        groups[i].rows = rows
+        r0 += rows
+    L = _lib.WalLayer()
+    L.in_features = in_features
+    L.out_features = r0
+    L.block_size = block
+    L.blocks_per_row = -(-in_features // block)
+    L.codebook_size = K
+    L.num_stages = S
+    L.id_dtype = id_dtype
+    L.codebook_dtype = _lib.F16
+    L.scale_dtype = _lib.F16
+    L.scale_rows = 1
+    L.n_groups = len(rows_per_group)
+    L.groups = ctypes.cast(groups, ctypes.POINTER(_lib.WalGroup))
+    L.plan = plan
+    return L, groups
+
+
+def test_plan_tables():
+    L, groups = _fake_layer([256, 256, 100])
+    lib = _lib.lib()
+    size = ctypes.c_size_t(0)
+    assert lib.wal_rvq_plan_size(ctypes.byref(L), ctypes.byref(size)) == 0
+    buf = (ctypes.c_uint8 * size.value)()
+    assert lib.wal_rvq_plan_build(ctypes.byref(L), buf, size.value) == 0
+    raw = bytes(buf)
+    magic, n_groups, goff, _ = struct.unpack_from("<4i", raw, 0)
+    toff = struct.unpack_from("<3i", raw, 16)
+    ntiles = struct.unpack_from("<3i", raw, 28)
+    assert magic == 0x57524C31 and n_groups == 3
+    # tile kinds of 16, 64 and 128 rows; tiles never straddle groups
+    assert ntiles == (16 + 16 + 7, 4 + 4 + 2, 2 + 2 + 1)
+    t128 = [struct.unpack_from("<4i", raw, toff[2] + 16 * i) for i in range(ntiles[2])]
+    assert t128 == [(0, 0, 128, 0), (0, 128, 128, 128), (1, 0, 128, 256), (1, 128, 128, 384), (2, 0, 100, 512)]
+    t16 = [struct.unpack_from("<4i", raw, toff[0] + 16 * i) for i in range(ntiles[0])]
+    assert t16[-1] == (2, 96, 4, 608)
+    # the group table is a verbatim copy of the host array
+    g2 = raw[goff + 2 * ctypes.sizeof(_lib.WalGroup): goff + 3 * ctypes.sizeof(_lib.WalGroup)]
+    assert g2 == bytes(groups[2])
+    # too small a buffer is refused
+    assert lib.wal_rvq_plan_build(ctypes.byref(L), buf, size.value - 1) == _lib.ESIZE
+
+
+@pytest.mark.parametrize("mutate,code,needle", [
+    (lambda L: setattr(L, "num_stages", 9), _lib.EINVAL, "num_stages"),
+    (lambda L: setattr(L, "codebook_size", 300), _lib.EINVAL, "does not fit"),
+    (lambda L: setattr(L, "out_features", 999), _lib.EINVAL, "cover"),
+    (lambda L: setattr(L, "blocks_per_row", 1), _lib.EINVAL, "in_features"),
+    (lambda L: setattr(L, "id_dtype", 7), _lib.EINVAL, "id dtype"),
+    (lambda L: setattr(L, "scale_rows", 0), _lib.EINVAL, "scale_rows"),
+])
+def test_linear_refuses_bad_layers(mutate, code, needle):
+    L, _g = _fake_layer([64])
+    mutate(L)
+    lib = _lib.lib()
+    rc = lib.wal_rvq_linear(ctypes.byref(L), 0, 0, 0x1000, 1, _lib.BF16, None, _lib.F32, 0x2000, _lib.BF16, None)
+    assert rc == code
+    assert needle in lib.wal_last_error().decode()
+
+
+def test_multi_group_needs_plan():
+    L, _g = _fake_layer([64, 64])
+    lib = _lib.lib()
+    rc = lib.wal_rvq_reconstruct(ctypes.byref(L), 0, 0, 0x1000, _lib.BF16, None)
+    assert rc == _lib.EINVAL and "plan" in lib.wal_last_error().decode()
+
+
+def test_gaps_between_groups_refused():
+    L, groups = _fake_layer([64, 64])
+    groups[1].row0 = 65
+    L.plan = 0x5000
+    lib = _lib.lib()
+    rc = lib.wal_rvq_reconstruct(ctypes.byref(L), 0, 0, 0x1000, _lib.BF16, None)
+    assert rc == _lib.EINVAL and "starts at row" in lib.wal_last_error().decode()
+
+
+def test_null_arguments_refused():
+    lib = _lib.lib()
+    assert lib.wal_rvq_linear(None, 0, 0, 0x1000, 1, _lib.BF16, None, _lib.F32, 0x2000, _lib.BF16, None) == _lib.EINVAL
+    L, _g = _fake_layer([64])
+    assert lib.wal_rvq_linear(ctypes.byref(L), 0, 0, None, 1, _lib.BF16, None, _lib.F32, 0x2000, _lib.BF16,
+                              None) == _lib.EINVAL
+    assert lib.wal_rvq_linear(ctypes.byref(L), 5, 0, 0x1000, 1, _lib.BF16, None, _lib.F32, 0x2000, _lib.BF16,
+                              None) == _lib.EINVAL
+    # m == 0 is a no-op that touches nothing
+    assert lib.wal_rvq_linear(ctypes.byref(L), 0, 0, 0x1000, 0, _lib.BF16, None, _lib.F32, 0x2000, _lib.BF16,
+                              None) == _lib.OK
+
+
+def test_triton_matmul_feature_mismatch():
+    lib = _lib.lib()
+    rc = lib.wal_rvq_group_linear_matmul(0x1000, 1, 100, _lib.BF16, 0x2000, _lib.U8, 2, 64, 3, 0x3000, _lib.F16,
+                                         256, 32, 0x4000, _lib.F16, 0x5000, _lib.BF16, None)
+    assert rc == _lib.EINVAL and "Feature mismatch" in lib.wal_last_error().decode()
+
+
+def test_id_route_argument_checks():
+    lib = _lib.lib()
+    rc = lib.wal_id_route_linear(0x1000, 1, 64, _lib.BF16, 0x2000, _lib.U8, 8, 0x3000, 100, _lib.F16, 0x4000,
+                                 None, _lib.F32, 0, 0x5000, _lib.BF16, None)
+    assert rc == _lib.EINVAL and "id dtype" in lib.wal_last_error().decode()
+    rc = lib.wal_id_route_linear(0x1000, 1, 64, _lib.BF16, 0x2000, _lib.I16, 8, 0x3000, 100, _lib.F16, 0x4000,
+                                 None, _lib.F32, 2, 0x5000, _lib.BF16, None)
+    assert rc == _lib.EINVAL and "mode" in lib.wal_last_error().decode()

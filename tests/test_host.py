@@ -1,0 +1,185 @@
+"""Host-side mirror of the reference interface, on the CPU: module structure,
+state_dict keys, constructor validation, stage controls, persistence format,
+storage accounting and the refusal to compute anywhere but on a ROCm GPU."""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import pytest
+import torch
+from torch import nn
+
+import wal2026_amd as w
+from _cases import make_encoding
+from wal2026_amd import synth
+from wal2026_amd.runtime import MATMUL_STRATEGIES
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def test_state_dict_keys_and_dtypes():
+    enc = make_encoding(96, 64, S=3, group_rows=32, stage_scales=True, seed=1)
+    mod = w.PackedGroupedBlockRVQLinear(enc, torch.randn(96))
+    sd = mod.state_dict()
+    for g in range(3):
+        for s in range(3):
+            assert sd[f"groups.{g}.stage_ids_{s}"].dtype == torch.uint8
+            assert sd[f"groups.{g}.codebook_{s}"].dtype == torch.float16
+        assert sd[f"groups.{g}.row_scale"].shape == (32, 1)
+        assert sd[f"groups.{g}.stage_scales"].dtype == torch.float16
+    assert sd["bias"].dtype == torch.bfloat16  # src/runtime.py:1229-1230
+    assert mod.in_features == 64 and mod.out_features == 96
+    assert mod.row_slices == ((0, 32), (32, 64), (64, 96))
+    # caches are plain attributes, not state
+    assert not any("desc" in k or "triton" in k for k in sd)
+    # round trip into a fresh module
+    mod2 = w.PackedGroupedBlockRVQLinear(make_encoding(96, 64, S=3, group_rows=32, stage_scales=True, seed=2),
+                                         torch.zeros(96))
+    mod2.load_state_dict(sd)
+    assert torch.equal(mod2.groups[1].stage_ids_2, mod.groups[1].stage_ids_2)
+
+
+def test_strategy_whitelist_and_messages():
+    enc = make_encoding(16, 32, S=1, seed=1)
+    for s in MATMUL_STRATEGIES:
+        kw = {}
+        if s == "chunked_weight":
+            kw["matmul_chunk_rows"] = 8
+        if "hot" in s:
+            kw["hot_topk"] = 4
+        if s == "local_palette":
+            kw["local_palette_group_cols"] = 8
+        w.PackedGroupedBlockRVQLinear(enc, matmul_strategy=s, **kw)
+    with pytest.raises(ValueError, match="unsupported matmul_strategy: nope"):
+        w.PackedGroupedBlockRVQLinear(enc, matmul_strategy="nope")
+    with pytest.raises(ValueError, match="chunked_weight requires a positive matmul_chunk_rows"):
+        w.PackedGroupedBlockRVQLinear(enc, matmul_strategy="chunked_weight")
+    with pytest.raises(ValueError, match="full_weight_hot requires a positive hot_topk"):
+        w.PackedGroupedBlockRVQLinear(enc, matmul_strategy="full_weight_hot")
+    # triton_hot_cold_persistent defaults its palette width like the reference
+    m = w.PackedGroupedBlockRVQLinear(enc, matmul_strategy="triton_hot_cold_persistent", hot_topk=2)
+    assert m.local_palette_group_cols == 256
+
+
+def test_forward_on_cpu_fails_loudly():
+    enc = make_encoding(16, 32, S=1, seed=1)
+    mod = w.PackedGroupedBlockRVQLinear(enc)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mod(torch.zeros(1, 32, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mod.reconstruct_weight(torch.bfloat16)
+    route = w.PackedIDRouteLinear(torch.zeros(4, 8, dtype=torch.int32), torch.ones(3, 2), torch.ones(4, 1))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        route(torch.zeros(1, 8))
+
+
+def test_unported_strategies_raise():
+    enc = make_encoding(16, 32, S=1, seed=1)
+    for s, kw in [("stagewise_einsum", {}), ("full_weight_hot", {"hot_topk": 2})]:
+        mod = w.PackedGroupedBlockRVQLinear(enc, matmul_strategy=s, **kw)
+        with pytest.raises(NotImplementedError):
+            mod(torch.zeros(1, 32))
+
+
+def test_active_stage_indices_match_fixture():
+    data = json.loads((GOLDEN / "active_stages.json").read_text())
+    for item in data:
+        spl = tuple(item["stages_per_split"]) or ()
+        S = max(sum(spl), 1)
+        enc = make_encoding(8, 16, S=S, K=16, stages_per_split=spl or (S,), product_splits=max(len(spl), 1), seed=0)
+        g = w.PackedBlockRVQGroup(enc.groups[0])
+        g.stages_per_split = spl
+        g.set_effective_stages_per_split(item["effective"])
+        assert list(g._compute_active_stage_indices()) == item["expected"], item
+
+
+class _Block(nn.Module):
+    def __init__(self, enc_attn, enc_mlp):
+        super().__init__()
+        self.self_attn = nn.Module()
+        self.self_attn.q_proj = w.PackedGroupedBlockRVQLinear(enc_attn)
+        self.mlp = nn.Module()
+        self.mlp.up_proj = w.PackedGroupedBlockRVQLinear(enc_mlp)
+
+
+def test_stage_setters():
+    model = nn.Module()
+    model.layers = nn.ModuleList([_Block(make_encoding(16, 32, S=3, group_rows=8, seed=i),
+                                         make_encoding(32, 32, S=3, seed=i)) for i in range(2)])
+    assert w.set_global_effective_stages(model, 2) == 2 * (2 + 1)
+    counts = w.set_effective_stages_by_name(model, 1, 3)
+    assert counts == {"attn": 2, "mlp": 2, "other": 0}
+    assert model.layers[0].self_attn.q_proj.groups[1]._compute_active_stage_indices() == (0,)
+    assert model.layers[0].mlp.up_proj.groups[0]._compute_active_stage_indices() == (0, 1, 2)
+    n = w.set_effective_stages_from_map(model, {"layers.1.mlp.up_proj": 2, "missing": 1})
+    assert n == 1
+    assert model.layers[1].mlp.up_proj.groups[0].active_stage_mask() == 0b011
+
+
+def test_encoding_io_round_trip(tmp_path):
+    enc = make_encoding(40, 24, d=8, S=2, K=64, group_rows=16, block_scale=True, seed=3)
+    path = w.save_grouped_encoding_map(tmp_path / "enc.pt", {"layers.0.mlp.up_proj": enc})
+    raw = torch.load(path, weights_only=True)
+    assert raw["version"] == 1 and set(raw["encodings"]) == {"layers.0.mlp.up_proj"}
+    assert set(raw["encodings"]["layers.0.mlp.up_proj"]) == {"groups", "row_slices", "original_shape"}
+    back = w.load_grouped_encoding_map(path)["layers.0.mlp.up_proj"]
+    assert back.row_slices == enc.row_slices and back.original_shape == enc.original_shape
+    for a, b in zip(back.groups, enc.groups):
+        assert all(torch.equal(x, y) for x, y in zip(a.stage_ids, b.stage_ids))
+        assert torch.equal(a.block_scale, b.block_scale)
+        assert a.padded_cols == b.padded_cols and a.stages_per_split == b.stages_per_split
+    bad = dict(raw, version=2)
+    torch.save(bad, tmp_path / "v2.pt")
+    with pytest.raises(ValueError, match="unsupported encoding map version"):
+        w.load_grouped_encoding_map(tmp_path / "v2.pt")
+
+
+def test_storage_accounting_matches_benchmark_arithmetic():
+    """The algorithmic bytes the roofline uses (ids + codebooks + scales)."""
+    assert synth.CONFIGS["c1"].compressed_bytes_per_layer() == 1_060_864
+    assert synth.CONFIGS["c2"].compressed_bytes_per_layer() == 15_308_800
+    assert synth.CONFIGS["c3"].compressed_bytes_per_layer() == 55_070_720
+    assert synth.CONFIGS["c5"].compressed_bytes_per_layer() == 89_875_456
+    assert synth.CONFIGS["c4"].flops_per_layer() == 893_353_197_568
+    cfg = synth.CONFIGS["c1"]
+    enc = synth.make_encoding(2048, 2048, cfg, synth.generator(0))
+    assert enc.storage_bytes() == 1_060_864
+    assert enc.bits_per_weight() == pytest.approx(8 * 1_060_864 / 2048**2)
+
+
+def test_synth_formats():
+    cfg = synth.CONFIGS["c3"]
+    enc = synth.make_encoding(256, 128, cfg, synth.generator(0))
+    g = enc.groups[0]
+    assert g.stage_ids[0].dtype == torch.int16 and len(g.stage_ids) == 1
+    assert int(g.stage_ids[0].max()) < 4096 and int(g.stage_ids[0].min()) >= 0
+    rs = g.row_scale.reshape(-1)
+    assert torch.equal(rs[:128], rs[0].expand(128)) and not torch.equal(rs[:128], rs[128:])
+    cfg5 = synth.CONFIGS["c5"]
+    enc5 = synth.make_encoding(600, 64, cfg5, synth.generator(0))
+    assert [tuple(s) for s in enc5.row_slices] == [(0, 256), (256, 512), (512, 600)]
+    assert enc5.groups[0].row_scale.dtype == torch.bfloat16
+
+
+def test_encoder_shapes_and_quality():
+    g = torch.Generator().manual_seed(0)
+    weight = torch.randn(64, 40, generator=g)
+    enc = w.encode_grouped_block_residual_vq(weight, group_rows=32, block_size=8, codebook_size=32, num_stages=2,
+                                             sample_limit=4096, kmeans_iters=4)
+    assert len(enc.groups) == 2 and enc.groups[0].stage_ids[0].shape == (32, 5)
+    assert enc.groups[0].stage_ids[0].dtype == torch.uint8
+    assert enc.groups[0].codebooks[0].dtype == torch.float16
+    assert 0.0 < enc.sample_rel_mse < 0.5
+    with pytest.raises(NotImplementedError):
+        w.encode_block_residual_vq(weight, transform_kind="dct")
+    with pytest.raises(ValueError):
+        w.encode_block_residual_vq(weight, product_splits=3, block_size=8)
+
+
+def test_kernel_functions_validate_like_the_reference():
+    x = torch.zeros(1, 64)
+    with pytest.raises(ValueError, match="expects CUDA tensors"):
+        w.rvq_group_linear_matmul(x, torch.zeros(2, 4, 2, dtype=torch.uint8), torch.zeros(2, 8, 32), torch.ones(4))
+    with pytest.raises(ValueError, match="expects CUDA tensors"):
+        w.id_route_linear_matmul(x, torch.zeros(4, 64, dtype=torch.int16), torch.zeros(8), torch.ones(4))

@@ -1,0 +1,418 @@
+// capi.hip -- the extern "C" entry points of libwal2026_amd.so.
+//
+// Every argument is validated on the host before a launch, so a malformed
+// call returns an error code instead of reaching a kernel.  Shapes a kernel
+// relies on (tile counts, alignment, LDS budget) are derived here.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/wal2026_amd.h"
+#include "rvq_kernels.h"
+
+using namespace wal;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(WAL_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool is_float_dtype(int dt) { return dt == WAL_F16 || dt == WAL_BF16 || dt == WAL_F32; }
+bool is_half_dtype(int dt) { return dt == WAL_F16 || dt == WAL_BF16; }
+bool is_id_dtype(int dt) { return dt == WAL_U8 || dt == WAL_I16 || dt == WAL_U16 || dt == WAL_I32; }
+
+int64_t id_capacity(int dt) {
+  switch (dt) {
+    case WAL_U8: return 256;
+    case WAL_I16: return 32767;
+    case WAL_U16: return 65536;
+    default: return 2147483647LL;
+  }
+}
+
+int id_bytes(int dt) { return dt == WAL_U8 ? 1 : (dt == WAL_I32 ? 4 : 2); }
+int float_bytes(int dt) { return dt == WAL_F32 ? 4 : 2; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int validate_layer(const wal_rvq_layer* Lh) {
+  if (!Lh) return fail(WAL_EINVAL, "layer is NULL");
+  const wal_rvq_layer& L = *Lh;
+  if (L.in_features < 1 || L.out_features < 1)
+    return fail(WAL_EINVAL, "in_features/out_features must be >= 1 (got %d, %d)", L.in_features, L.out_features);
+  if (L.block_size < 1 || L.blocks_per_row < 1)
+    return fail(WAL_EINVAL, "block_size/blocks_per_row must be >= 1");
+  if ((int64_t)L.blocks_per_row * L.block_size < L.in_features)
+    return fail(WAL_EINVAL, "blocks_per_row * block_size (%lld) < in_features (%d)",
+                (long long)L.blocks_per_row * L.block_size, L.in_features);
+  if (L.num_stages < 1 || L.num_stages > WAL_RVQ_MAX_STAGES)
+    return fail(WAL_EINVAL, "num_stages must be in [1, %d] (got %d)", WAL_RVQ_MAX_STAGES, L.num_stages);
+  if (!is_id_dtype(L.id_dtype)) return fail(WAL_EINVAL, "bad id dtype %d", L.id_dtype);
+  if (!is_float_dtype(L.codebook_dtype)) return fail(WAL_EINVAL, "bad codebook dtype %d", L.codebook_dtype);
+  if (!is_float_dtype(L.scale_dtype)) return fail(WAL_EINVAL, "bad scale dtype %d", L.scale_dtype);
+  if (L.codebook_size < 1) return fail(WAL_EINVAL, "codebook_size must be >= 1");
+  if (L.codebook_size > id_capacity(L.id_dtype))
+    return fail(WAL_EINVAL, "codebook_size %d does not fit id dtype %d", L.codebook_size, L.id_dtype);
+  if (L.scale_rows < 1) return fail(WAL_EINVAL, "scale_rows must be >= 1");
+  if (L.n_groups < 1 || !L.groups) return fail(WAL_EINVAL, "layer has no groups");
+  int64_t next = 0;
+  for (int g = 0; g < L.n_groups; ++g) {
+    const wal_rvq_group& G = L.groups[g];
+    if (G.rows < 1) return fail(WAL_EINVAL, "group %d has %d rows", g, G.rows);
+    if (G.row0 != next) return fail(WAL_EINVAL, "group %d starts at row %d, expected %lld", g, G.row0, (long long)next);
+    next += G.rows;
+    for (int s = 0; s < L.num_stages; ++s)
+      if (!G.stage_ids[s] || !G.codebooks[s]) return fail(WAL_EINVAL, "group %d stage %d has a NULL buffer", g, s);
+    if (!G.row_scale) return fail(WAL_EINVAL, "group %d has no row_scale", g);
+  }
+  if (next != L.out_features)
+    return fail(WAL_EINVAL, "groups cover %lld rows, out_features is %d", (long long)next, L.out_features);
+  if (L.n_groups > 1 && !L.plan) return fail(WAL_EINVAL, "a layer with %d groups needs a plan", L.n_groups);
+  return WAL_OK;
+}
+
+struct PlanLayout {
+  size_t groups_offset;
+  size_t tiles_offset[kNumTileKinds];
+  int32_t n_tiles[kNumTileKinds];
+  size_t bytes;
+};
+
+PlanLayout plan_layout(const wal_rvq_layer& L) {
+  PlanLayout P;
+  size_t off = (sizeof(PlanHeader) + 15) & ~size_t(15);
+  P.groups_offset = off;
+  off += sizeof(wal_rvq_group) * L.n_groups;
+  for (int k = 0; k < kNumTileKinds; ++k) {
+    int64_t n = 0;
+    for (int g = 0; g < L.n_groups; ++g) n += ceil_div(L.groups[g].rows, kTileRows[k]);
+    P.n_tiles[k] = (int32_t)n;
+    off = (off + 15) & ~size_t(15);
+    P.tiles_offset[k] = off;
+    off += sizeof(PlanTile) * n;
+  }
+  P.bytes = off;
+  return P;
+}
+
+int n_tiles_of(const wal_rvq_layer& L, int kind) {
+  int64_t n = 0;
+  for (int g = 0; g < L.n_groups; ++g) n += ceil_div(L.groups[g].rows, kTileRows[kind]);
+  return (int)n;
+}
+
+LayerArgs make_args(const wal_rvq_layer& L, int kind, uint32_t active_mask) {
+  LayerArgs A;
+  memset(&A, 0, sizeof(A));
+  A.in_features = L.in_features;
+  A.out_features = L.out_features;
+  A.block_size = L.block_size;
+  A.blocks_per_row = L.blocks_per_row;
+  A.codebook_size = L.codebook_size;
+  A.num_stages = L.num_stages;
+  A.scale_rows = L.scale_rows;
+  A.tile_kind = kind;
+  A.tile_rows = kTileRows[kind];
+  A.n_tiles = n_tiles_of(L, kind);
+  A.active_mask = active_mask;
+  A.plan = L.n_groups > 1 ? reinterpret_cast<const PlanHeader*>(L.plan) : nullptr;
+  A.g0 = L.groups[0];
+  return A;
+}
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// LDS form of the codebooks for the MFMA kernels.
+int lds_mode_for(const wal_rvq_layer& L, int sem) {
+  if (sem == SEM_FAST || L.num_stages == 1) return LM_A16;
+  bool any_ss = false;
+  for (int g = 0; g < L.n_groups; ++g) any_ss |= L.groups[g].stage_scales != nullptr;
+  return (L.codebook_dtype == WAL_F16 && !any_ss) ? LM_H16 : LM_F32;
+}
+
+// True when the block-size-8 MFMA kernels can run this layer.
+bool mfma_eligible(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, bool prefill) {
+  if (L.block_size != 8 || (int64_t)L.blocks_per_row * 8 != L.in_features) return false;
+  if (L.blocks_per_row % 16 != 0) return false;
+  if (L.num_stages > 4) return false;
+  if (L.id_dtype == WAL_I32) return false;
+  if (!is_half_dtype(x_dtype) || !aligned16(x)) return false;
+  for (int g = 0; g < L.n_groups; ++g) {
+    const wal_rvq_group& G = L.groups[g];
+    if (G.block_scale) return false;
+    for (int s = 0; s < L.num_stages; ++s)
+      if (!aligned16(G.stage_ids[s]) || !aligned16(G.codebooks[s])) return false;
+  }
+  const int esz = lds_mode_for(L, sem) == LM_F32 ? 32 : 16;
+  const size_t cb = (size_t)L.num_stages * L.codebook_size * esz;
+  const size_t budget = prefill ? (160 * 1024 - 4 * 128 * 72 * 2) : (160 * 1024 - 8 * 1024);
+  return cb <= budget;
+}
+
+// Resolve FAST on groups that are not "plain" (src/runtime.py:416-429, :579-580).
+int resolve_semantics(const wal_rvq_layer& L, int semantics, int* sem) {
+  if (semantics == WAL_RVQ_RECONSTRUCT) {
+    *sem = SEM_RECON;
+    return WAL_OK;
+  }
+  if (semantics != WAL_RVQ_RECONSTRUCT_FAST) return fail(WAL_EINVAL, "unknown semantics %d", semantics);
+  int with_bs = 0;
+  for (int g = 0; g < L.n_groups; ++g) with_bs += L.groups[g].block_scale != nullptr;
+  if (with_bs == 0) *sem = SEM_FAST;
+  else if (with_bs == L.n_groups) *sem = SEM_RECON;
+  else return fail(WAL_EUNSUPPORTED, "RECONSTRUCT_FAST on a layer where only some groups have block_scale");
+  return WAL_OK;
+}
+
+uint32_t resolve_mask(const wal_rvq_layer& L, uint32_t mask) {
+  const uint32_t all = (L.num_stages >= 32) ? 0xffffffffu : ((1u << L.num_stages) - 1u);
+  mask &= all;
+  return mask ? mask : all;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wal_last_error(void) { return g_err; }
+
+int wal_abi_version(void) { return WAL_ABI_VERSION; }
+
+int wal_rvq_plan_size(const wal_rvq_layer* layer, size_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return fail(WAL_EINVAL, "bytes is NULL");
+  if (!layer || layer->n_groups < 1 || !layer->groups) return fail(WAL_EINVAL, "layer has no groups");
+  *bytes = plan_layout(*layer).bytes;
+  return WAL_OK;
+}
+
+int wal_rvq_plan_build(const wal_rvq_layer* layer, void* dst, size_t bytes) {
+  g_err[0] = 0;
+  if (!layer || layer->n_groups < 1 || !layer->groups) return fail(WAL_EINVAL, "layer has no groups");
+  if (!dst) return fail(WAL_EINVAL, "dst is NULL");
+  const PlanLayout P = plan_layout(*layer);
+  if (bytes < P.bytes) return fail(WAL_ESIZE, "plan needs %zu bytes, got %zu", P.bytes, bytes);
+  memset(dst, 0, P.bytes);
+  char* base = static_cast<char*>(dst);
+  PlanHeader* H = reinterpret_cast<PlanHeader*>(base);
+  H->magic = kPlanMagic;
+  H->n_groups = layer->n_groups;
+  H->groups_offset = (int32_t)P.groups_offset;
+  memcpy(base + P.groups_offset, layer->groups, sizeof(wal_rvq_group) * layer->n_groups);
+  for (int k = 0; k < kNumTileKinds; ++k) {
+    H->tiles_offset[k] = (int32_t)P.tiles_offset[k];
+    H->n_tiles[k] = P.n_tiles[k];
+    PlanTile* T = reinterpret_cast<PlanTile*>(base + P.tiles_offset[k]);
+    int i = 0;
+    for (int g = 0; g < layer->n_groups; ++g) {
+      const wal_rvq_group& G = layer->groups[g];
+      for (int r = 0; r < G.rows; r += kTileRows[k]) {
+        T[i].group = g;
+        T[i].row0 = r;
+        T[i].rows = (G.rows - r) < kTileRows[k] ? (G.rows - r) : kTileRows[k];
+        T[i].out_row0 = G.row0 + r;
+        ++i;
+      }
+    }
+  }
+  return WAL_OK;
+}
+
+int wal_rvq_reconstruct(const wal_rvq_layer* layer, int semantics, uint32_t active_stage_mask, void* w_out,
+                        int out_dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = validate_layer(layer);
+  if (rc) return rc;
+  if (!w_out) return fail(WAL_EINVAL, "w_out is NULL");
+  if (!is_float_dtype(out_dtype)) return fail(WAL_EINVAL, "bad out dtype %d", out_dtype);
+  int sem = 0;
+  if ((rc = resolve_semantics(*layer, semantics, &sem))) return rc;
+  LayerArgs A = make_args(*layer, 0, resolve_mask(*layer, active_stage_mask));
+  DtypeArgs D{layer->id_dtype, layer->codebook_dtype, layer->scale_dtype, out_dtype};
+  hipError_t e = launch_dequant(A, D, sem, w_out, out_dtype, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_reconstruct launch");
+}
+
+int wal_rvq_linear(const wal_rvq_layer* layer, int semantics, uint32_t active_stage_mask, const void* x, int64_t m,
+                   int x_dtype, const void* bias, int bias_dtype, void* y, int y_dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = validate_layer(layer);
+  if (rc) return rc;
+  if (m < 0) return fail(WAL_EINVAL, "m must be >= 0");
+  if (m == 0) return WAL_OK;
+  if (!x || !y) return fail(WAL_EINVAL, "x and y must not be NULL");
+  if (!is_float_dtype(x_dtype)) return fail(WAL_EINVAL, "bad x dtype %d", x_dtype);
+  if (!is_float_dtype(y_dtype)) return fail(WAL_EINVAL, "bad y dtype %d", y_dtype);
+  if (bias && !is_float_dtype(bias_dtype)) return fail(WAL_EINVAL, "bad bias dtype %d", bias_dtype);
+  int sem = 0;
+  if ((rc = resolve_semantics(*layer, semantics, &sem))) return rc;
+  const uint32_t mask = resolve_mask(*layer, active_stage_mask);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  DtypeArgs D{layer->id_dtype, layer->codebook_dtype, layer->scale_dtype, x_dtype};
+  EpilogueArgs E{y, bias, (int64_t)layer->out_features, y_dtype, x_dtype, bias_dtype, bias ? 1 : 0};
+  hipError_t e;
+  if (m <= 16 && mfma_eligible(*layer, sem, x_dtype, x, false)) {
+    LayerArgs A = make_args(*layer, 0, mask);
+    e = launch_decode(A, D, E, sem, lds_mode_for(*layer, sem), x, (int)m, device_cu_count(), st);
+  } else if (m > 16 && mfma_eligible(*layer, sem, x_dtype, x, true)) {
+    LayerArgs A = make_args(*layer, 2, mask);
+    e = launch_prefill(A, D, E, sem, lds_mode_for(*layer, sem), x, m, st);
+  } else {
+    LayerArgs A = make_args(*layer, 1, mask);
+    e = launch_generic_linear(A, D, E, sem, x, m, st);
+  }
+  return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_linear launch");
+}
+
+int wal_rvq_group_linear_matmul(const void* x, int64_t m, int64_t k_in, int x_dtype, const void* stage_ids,
+                                int id_dtype, int32_t num_stages, int64_t n, int64_t blocks_per_row,
+                                const void* codebooks, int cb_dtype, int64_t codebook_size, int32_t block_size,
+                                const void* row_scale, int rs_dtype, void* out, int out_dtype, void* stream) {
+  g_err[0] = 0;
+  if (!x || !stage_ids || !codebooks || !row_scale || !out) return fail(WAL_EINVAL, "NULL buffer");
+  if (m < 0 || n < 1 || k_in < 1 || blocks_per_row < 1 || block_size < 1 || codebook_size < 1)
+    return fail(WAL_EINVAL, "bad shape");
+  if (num_stages < 1 || num_stages > WAL_RVQ_MAX_STAGES) return fail(WAL_EINVAL, "bad stage count %d", num_stages);
+  // src/triton_id_matmul.py:246-248: the padded width must equal x's width
+  if (blocks_per_row * block_size != k_in)
+    return fail(WAL_EINVAL, "Feature mismatch: expected %lld, got %lld", (long long)(blocks_per_row * block_size),
+                (long long)k_in);
+  if (!is_float_dtype(x_dtype)) return fail(WAL_EINVAL, "bad x dtype");
+  if (!is_id_dtype(id_dtype) || !is_half_dtype(cb_dtype) || !is_float_dtype(rs_dtype) || !is_float_dtype(out_dtype))
+    return fail(WAL_EINVAL, "bad dtype");
+  if (codebook_size > id_capacity(id_dtype)) return fail(WAL_EINVAL, "codebook_size does not fit id dtype");
+  if (n > 0x7fffffff || k_in > 0x7fffffff) return fail(WAL_EINVAL, "shape too large");
+  if (m == 0) return WAL_OK;
+  wal_rvq_group G;
+  memset(&G, 0, sizeof(G));
+  for (int s = 0; s < num_stages; ++s) {
+    G.stage_ids[s] = static_cast<const char*>(stage_ids) + (size_t)s * n * blocks_per_row * id_bytes(id_dtype);
+    G.codebooks[s] = static_cast<const char*>(codebooks) + (size_t)s * codebook_size * block_size * float_bytes(cb_dtype);
+  }
+  G.row_scale = row_scale;
+  G.row0 = 0;
+  G.rows = (int32_t)n;
+  wal_rvq_layer L;
+  memset(&L, 0, sizeof(L));
+  L.in_features = (int32_t)k_in;
+  L.out_features = (int32_t)n;
+  L.block_size = block_size;
+  L.blocks_per_row = (int32_t)blocks_per_row;
+  L.codebook_size = (int32_t)codebook_size;
+  L.num_stages = num_stages;
+  L.id_dtype = id_dtype;
+  L.codebook_dtype = cb_dtype;
+  L.scale_dtype = rs_dtype;
+  L.scale_rows = 1;
+  L.n_groups = 1;
+  L.groups = &G;
+  LayerArgs A = make_args(L, 1, 0);
+  DtypeArgs D{id_dtype, cb_dtype, rs_dtype, x_dtype};
+  EpilogueArgs E{out, nullptr, n, out_dtype, x_dtype, WAL_F32, 0};
+  hipError_t e = launch_generic_linear(A, D, E, SEM_TRITON, x, m, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_group_linear_matmul launch");
+}
+
+int wal_id_route_linear(const void* x, int64_t m, int64_t k, int x_dtype, const void* ids, int id_dtype, int64_t n,
+                        const void* codebook_sum, int64_t routes, int cs_dtype, const void* row_scale,
+                        const void* bias, int bias_dtype, int mode, void* y, int y_dtype, void* stream) {
+  g_err[0] = 0;
+  if (!x || !ids || !codebook_sum || !row_scale || !y) return fail(WAL_EINVAL, "NULL buffer");
+  if (m < 0 || k < 1 || n < 1 || routes < 1) return fail(WAL_EINVAL, "bad shape");
+  if (n > 0x7fffffff || k > 0x7fffffff || routes > 0x7fffffff) return fail(WAL_EINVAL, "shape too large");
+  if (mode != 0 && mode != 1) return fail(WAL_EINVAL, "mode must be 0 or 1");
+  if (!is_float_dtype(x_dtype)) return fail(WAL_EINVAL, "bad x dtype");
+  if (!(id_dtype == WAL_I16 || id_dtype == WAL_U16 || id_dtype == WAL_I32)) return fail(WAL_EINVAL, "bad id dtype");
+  if (!is_half_dtype(cs_dtype) || !is_float_dtype(y_dtype)) return fail(WAL_EINVAL, "bad dtype");
+  if (bias && !is_float_dtype(bias_dtype)) return fail(WAL_EINVAL, "bad bias dtype");
+  if (m == 0) return WAL_OK;
+  wal_rvq_group G;
+  memset(&G, 0, sizeof(G));
+  G.stage_ids[0] = ids;
+  G.codebooks[0] = codebook_sum;
+  G.row_scale = row_scale;
+  G.rows = (int32_t)n;
+  wal_rvq_layer L;
+  memset(&L, 0, sizeof(L));
+  L.in_features = (int32_t)k;
+  L.out_features = (int32_t)n;
+  L.block_size = 1;
+  L.blocks_per_row = (int32_t)k;
+  L.codebook_size = (int32_t)routes;
+  L.num_stages = 1;
+  L.id_dtype = id_dtype;
+  L.codebook_dtype = cs_dtype;
+  L.scale_dtype = cs_dtype;
+  L.scale_rows = 1;
+  L.n_groups = 1;
+  L.groups = &G;
+  LayerArgs A = make_args(L, 1, 0);
+  DtypeArgs D{id_dtype, cs_dtype, cs_dtype, x_dtype};
+  EpilogueArgs E{y, bias, n, y_dtype, x_dtype, bias_dtype, bias ? (mode == 0 ? 1 : 2) : 0};
+  hipError_t e = launch_generic_linear(A, D, E, mode == 0 ? SEM_ROUTE0 : SEM_ROUTE1, x, m,
+                                       static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_id_route_linear launch");
+}
+
+int wal_id_route_reconstruct(const void* ids, int id_dtype, int64_t n, int64_t k, const void* codebook_sum,
+                             int64_t routes, int cs_dtype, const void* row_scale, int mode, int out_dtype, void* w_out,
+                             void* stream) {
+  g_err[0] = 0;
+  if (!ids || !codebook_sum || !row_scale || !w_out) return fail(WAL_EINVAL, "NULL buffer");
+  if (k < 1 || n < 1 || routes < 1) return fail(WAL_EINVAL, "bad shape");
+  if (n > 0x7fffffff || k > 0x7fffffff || routes > 0x7fffffff) return fail(WAL_EINVAL, "shape too large");
+  if (mode != 0 && mode != 1) return fail(WAL_EINVAL, "mode must be 0 or 1");
+  if (!(id_dtype == WAL_I16 || id_dtype == WAL_U16 || id_dtype == WAL_I32)) return fail(WAL_EINVAL, "bad id dtype");
+  if (!is_half_dtype(cs_dtype) || !is_float_dtype(out_dtype)) return fail(WAL_EINVAL, "bad dtype");
+  wal_rvq_group G;
+  memset(&G, 0, sizeof(G));
+  G.stage_ids[0] = ids;
+  G.codebooks[0] = codebook_sum;
+  G.row_scale = row_scale;
+  G.rows = (int32_t)n;
+  wal_rvq_layer L;
+  memset(&L, 0, sizeof(L));
+  L.in_features = (int32_t)k;
+  L.out_features = (int32_t)n;
+  L.block_size = 1;
+  L.blocks_per_row = (int32_t)k;
+  L.codebook_size = (int32_t)routes;
+  L.num_stages = 1;
+  L.id_dtype = id_dtype;
+  L.codebook_dtype = cs_dtype;
+  L.scale_dtype = cs_dtype;
+  L.scale_rows = 1;
+  L.n_groups = 1;
+  L.groups = &G;
+  LayerArgs A = make_args(L, 0, 0);
+  DtypeArgs D{id_dtype, cs_dtype, cs_dtype, out_dtype};
+  hipError_t e = launch_dequant(A, D, mode == 0 ? SEM_ROUTE0 : SEM_ROUTE1, w_out, out_dtype,
+                                static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_id_route_reconstruct launch");
+}
+
+}  // extern "C"

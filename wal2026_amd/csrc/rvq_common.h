@@ -1,0 +1,212 @@
+// rvq_common.h -- shared device code for the gfx950 Block-RVQ kernels.
+//
+// Every kernel reproduces the reference's dequantisation of one weight element
+// (src/runtime.py:379-414 for RECONSTRUCT, :568-598 for RECONSTRUCT_FAST):
+//
+//   RECONSTRUCT, output dtype dt:
+//     t  = ((0 + v_0) + v_1) + ... + v_{S-1}    fp32, v_s = f32(cb_s[id_s][j]) [* f32(stage_scale_s)]
+//     t  = t * f32(block_scale[r, b])            (if present)
+//     W  = rne_dt(rne_dt(t) * rne_dt(row_scale[r]))     (dt = f32: W = t * f32(row_scale))
+//   RECONSTRUCT_FAST, over the active stages s_0 < s_1 < ...:
+//     c_s = rne_dt(cb_s[id_s][j]) [then rne_dt(c_s * rne_dt(stage_scale_s))]
+//     a   = c_{s_0};  a = rne_dt(a + c_{s_k}) for k >= 1
+//     W   = rne_dt(a * rne_dt(row_scale[r]))
+//
+// Products of two values that are each exact in bf16/fp16 are exact in fp32,
+// so "round the fp32 product" equals torch's bf16/fp16 multiply.  The library
+// is compiled with -ffp-contract=off so no add/multiply pair is fused.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "wal2026_amd.h"
+
+namespace wal {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Plan image (built on the host by wal_rvq_plan_build, read by kernels).
+// ---------------------------------------------------------------------------
+constexpr int kPlanMagic = 0x57524c31;  // "WRL1"
+constexpr int kNumTileKinds = 3;
+constexpr int kTileRows[kNumTileKinds] = {16, 64, 128};
+
+struct PlanTile {
+  int32_t group;
+  int32_t row0;  // first row inside the group
+  int32_t rows;  // rows in this tile (<= tile size)
+  int32_t out_row0;  // first output row (group row0 + row0)
+};
+
+struct PlanHeader {
+  int32_t magic;
+  int32_t n_groups;
+  int32_t groups_offset;  // bytes from the header start
+  int32_t pad;
+  int32_t tiles_offset[kNumTileKinds];
+  int32_t n_tiles[kNumTileKinds];
+};
+
+// Kernel-side constants of one layer (passed by value).
+struct LayerArgs {
+  int32_t in_features;
+  int32_t out_features;
+  int32_t block_size;
+  int32_t blocks_per_row;
+  int32_t codebook_size;
+  int32_t num_stages;
+  int32_t scale_rows;
+  int32_t n_tiles;       // for the kernel's tile kind
+  int32_t tile_rows;     // rows per tile for the kernel's tile kind
+  int32_t tile_kind;
+  uint32_t active_mask;  // RECONSTRUCT_FAST active stages
+  int32_t pad;
+  const PlanHeader* plan;  // NULL -> single group g0
+  wal_rvq_group g0;
+};
+
+struct TileInfo {
+  wal_rvq_group g;  // by value: no pointer into the kernel-argument segment
+  int32_t group;
+  int32_t row0;      // first row inside the group
+  int32_t rows;
+  int32_t out_row0;  // first output row
+};
+
+__device__ inline TileInfo get_tile(const LayerArgs& L, int t) {
+  TileInfo ti;
+  if (L.plan == nullptr) {
+    ti.g = L.g0;
+    ti.group = 0;
+    ti.row0 = t * L.tile_rows;
+    ti.rows = min(L.tile_rows, L.g0.rows - ti.row0);
+    ti.out_row0 = L.g0.row0 + ti.row0;
+  } else {
+    const char* base = reinterpret_cast<const char*>(L.plan);
+    const PlanTile* tiles = reinterpret_cast<const PlanTile*>(base + L.plan->tiles_offset[L.tile_kind]);
+    const wal_rvq_group* groups = reinterpret_cast<const wal_rvq_group*>(base + L.plan->groups_offset);
+    PlanTile pt = tiles[t];
+    ti.g = groups[pt.group];
+    ti.group = pt.group;
+    ti.row0 = pt.row0;
+    ti.rows = pt.rows;
+    ti.out_row0 = pt.out_row0;
+  }
+  return ti;
+}
+
+// ---------------------------------------------------------------------------
+// Scalar conversions.
+// ---------------------------------------------------------------------------
+__device__ inline float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ inline float f16_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// fp32 -> bf16 round-to-nearest-even; NaN -> 0x7fc0 (torch's scalar rule).
+__device__ inline uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// fp32 -> fp16 round-to-nearest-even, subnormals and overflow per IEEE-754;
+// NaN -> sign | 0x7e00 (torch's scalar rule).
+__device__ inline uint32_t f32_to_f16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t sign = (u >> 16) & 0x8000u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7e00u;
+  if (a >= 0x477ff000u) return sign | 0x7c00u;
+  int e = (int)(a >> 23) - 127;
+  if (e >= -14) {
+    uint32_t man = a & 0x7fffffu;
+    uint32_t h = ((uint32_t)(e + 15) << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return sign | h;
+  }
+  if (e < -25) return sign;
+  uint32_t sig = (a & 0x7fffffu) | 0x800000u;
+  int s = -(e + 1);
+  uint32_t q = sig >> s;
+  uint32_t rem = sig & ((1u << s) - 1u);
+  uint32_t half = 1u << (s - 1);
+  if (rem > half || (rem == half && (q & 1u))) q++;
+  return sign | q;
+}
+
+template <int DT>
+__device__ inline float round_dt(float v) {
+  if constexpr (DT == WAL_BF16) return bf16_to_f32(f32_to_bf16_rne(v));
+  else if constexpr (DT == WAL_F16) return f16_to_f32(f32_to_f16_rne(v));
+  else return v;
+}
+
+template <int DT>
+__device__ inline uint32_t to_bits16(float v) {
+  if constexpr (DT == WAL_BF16) return f32_to_bf16_rne(v);
+  else return f32_to_f16_rne(v);
+}
+
+// Load element i of a float buffer of runtime dtype dt as fp32 (exact).
+__device__ inline float load_f(const void* p, int dt, int64_t i) {
+  if (dt == WAL_F16) return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  if (dt == WAL_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  return reinterpret_cast<const float*>(p)[i];
+}
+
+__device__ inline int64_t load_id(const void* p, int dt, int64_t i) {
+  if (dt == WAL_U8) return reinterpret_cast<const uint8_t*>(p)[i];
+  if (dt == WAL_I16) return reinterpret_cast<const int16_t*>(p)[i];
+  if (dt == WAL_U16) return reinterpret_cast<const uint16_t*>(p)[i];
+  return reinterpret_cast<const int32_t*>(p)[i];
+}
+
+// Hardware packed conversions (round-to-nearest-even for finite inputs).
+__device__ inline uint32_t pack_bf16(float lo, float hi) {
+  bf16x2_t r = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, r);
+}
+__device__ inline uint32_t pack_f16(float lo, float hi) {
+  f16x2_t r = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, r);
+}
+__device__ inline float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ inline float hi_bf16(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+__device__ inline float lo_f16(uint32_t p) { return f16_to_f32(p & 0xffffu); }
+__device__ inline float hi_f16(uint32_t p) { return f16_to_f32(p >> 16); }
+
+// f32(a.lo) + f32(b.lo) / f32(a.hi) + f32(b.hi) for packed fp16 pairs: one
+// v_fma_mix_f32 each (a * 1.0 + b, a single fp32 rounding == the fp32 add).
+__device__ inline float mix_add_lo(uint32_t a, uint32_t b) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ inline float mix_add_hi(uint32_t a, uint32_t b) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+// t + f32(a.lo) / t + f32(a.hi) for an fp32 t and a packed fp16 pair.
+__device__ inline float mix_acc_lo(float t, uint32_t a) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(a), "v"(t));
+  return r;
+}
+__device__ inline float mix_acc_hi(float t, uint32_t a) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(a), "v"(t));
+  return r;
+}
+
+}  // namespace wal

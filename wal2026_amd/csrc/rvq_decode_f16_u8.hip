@@ -1,0 +1,7 @@
+// decode kernel instantiations for f16 activations and 8-bit indices.
+#include "rvq_decode_impl.h"
+
+namespace wal {
+template hipError_t decode_entry<WAL_F16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&, int, int,
+                                              const void*, int M, int n_cu, hipStream_t);
+}  // namespace wal

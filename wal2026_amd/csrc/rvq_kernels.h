@@ -1,0 +1,95 @@
+// rvq_kernels.h -- declarations shared by the kernel files and the C API.
+#pragma once
+
+#include "rvq_common.h"
+
+namespace wal {
+
+// Arithmetic a kernel reproduces.
+enum Semantics : int {
+  SEM_RECON = 0,   // reconstruct_weight, src/runtime.py:379-414
+  SEM_FAST = 1,    // reconstruct_weight_fast, src/runtime.py:568-598
+  SEM_TRITON = 2,  // _rvq_group_linear_kernel, src/triton_id_matmul.py:186-216
+  SEM_ROUTE0 = 3,  // PackedIDRouteLinear.forward, src/runtime.py:89-97
+  SEM_ROUTE1 = 4   // _id_route_linear_kernel, src/triton_id_matmul.py:55-62
+};
+
+struct DtypeArgs {
+  int32_t id_dtype;
+  int32_t cb_dtype;
+  int32_t sc_dtype;  // row_scale / stage_scales / block_scale
+  int32_t x_dtype;
+};
+
+// Output stage.  bias_mode: 0 none; 1 y = round(acc + bias_x) (bias inside
+// F.linear); 2 y = round_x(round_x(acc) + bias_x) (bias added to the rounded
+// kernel output, src/runtime.py:103-104).  bias_x = bias rounded to x dtype
+// (the reference's `bias.to(x.dtype)`).
+struct EpilogueArgs {
+  void* y;
+  const void* bias;
+  int64_t ldy;
+  int32_t y_dtype;
+  int32_t x_dtype;
+  int32_t bias_dtype;
+  int32_t bias_mode;
+};
+
+__device__ inline float round_rt(float v, int dt) {
+  if (dt == WAL_BF16) return round_dt<WAL_BF16>(v);
+  if (dt == WAL_F16) return round_dt<WAL_F16>(v);
+  return v;
+}
+
+__device__ inline void store_output(const EpilogueArgs& E, int64_t m, int64_t n, float acc) {
+  float v = acc;
+  if (E.bias_mode != 0) {
+    const float b = round_rt(load_f(E.bias, E.bias_dtype, n), E.x_dtype);
+    if (E.bias_mode == 1) v = v + b;
+    else v = round_rt(v, E.x_dtype) + b;
+  }
+  const int64_t i = m * E.ldy + n;
+  if (E.y_dtype == WAL_F32) reinterpret_cast<float*>(E.y)[i] = v;
+  else if (E.y_dtype == WAL_BF16) reinterpret_cast<uint16_t*>(E.y)[i] = (uint16_t)f32_to_bf16_rne(v);
+  else reinterpret_cast<uint16_t*>(E.y)[i] = (uint16_t)f32_to_f16_rne(v);
+}
+
+// Launchers (defined in the .hip files; all return hipGetLastError()).
+hipError_t launch_dequant(const LayerArgs& L, const DtypeArgs& D, int sem, void* out, int out_dtype, hipStream_t st);
+hipError_t launch_generic_linear(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
+                                 const void* x, int64_t M, hipStream_t st);
+
+// Codebook form in LDS for the block-size-8 MFMA kernels (rvq_fragment.h);
+// capi.hip decides when those kernels apply (mfma_eligible).
+enum LdsMode : int { LM_A16 = 0, LM_H16 = 1, LM_F32 = 2 };
+
+template <int XDT, typename IdT>
+hipError_t decode_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
+                        const void* x, int M, int n_cu, hipStream_t st);
+template <int XDT, typename IdT>
+hipError_t prefill_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
+                         const void* x, int64_t M, hipStream_t st);
+
+inline hipError_t launch_decode(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
+                                int lds_mode, const void* x, int M, int n_cu, hipStream_t st) {
+  if (L.n_tiles == 0) return hipSuccess;
+  const bool wide = D.id_dtype != WAL_U8;
+  if (D.x_dtype == WAL_BF16)
+    return wide ? decode_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, n_cu, st)
+                : decode_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, n_cu, st);
+  return wide ? decode_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, n_cu, st)
+              : decode_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, n_cu, st);
+}
+
+inline hipError_t launch_prefill(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
+                                 int lds_mode, const void* x, int64_t M, hipStream_t st) {
+  if (L.n_tiles == 0 || M == 0) return hipSuccess;
+  const bool wide = D.id_dtype != WAL_U8;
+  if (D.x_dtype == WAL_BF16)
+    return wide ? prefill_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, st)
+                : prefill_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, st);
+  return wide ? prefill_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, st)
+              : prefill_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, st);
+}
+
+}  // namespace wal
