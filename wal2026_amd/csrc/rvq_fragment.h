@@ -39,7 +39,19 @@ __device__ inline void stage_codebooks(uint8_t* lds, const wal_rvq_group& g, int
       for (int j = 0; j < 4; ++j) { v[j] = __uint_as_float(a[j]); v[4 + j] = __uint_as_float(b[j]); }
     } else {
       u32x4_t a = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(cb) + (int64_t)k * 8);
-      if (LMODE == LM_H16) {  // raw fp16 copy
+      if (LMODE == LM_H16) {
+        // fp16 copy.  Stage 0 is stored as 0 + v (-0 becomes +0), the first
+        // add of the reference's zero-initialised fp32 sum, so the fragment
+        // code can sum the stages without a leading zero.
+        if (s == 0) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            uint32_t w = a[j];
+            if ((w & 0xffffu) == 0x8000u) w &= 0xffff0000u;
+            if ((w >> 16) == 0x8000u) w &= 0x0000ffffu;
+            a[j] = w;
+          }
+        }
         *reinterpret_cast<u32x4_t*>(lds + (size_t)e * 16) = a;
         continue;
       }
@@ -53,11 +65,13 @@ __device__ inline void stage_codebooks(uint8_t* lds, const wal_rvq_group& g, int
     const bool has_ss = g.stage_scales != nullptr;
     const float ss = has_ss ? load_f(g.stage_scales, D.sc_dtype, s) : 1.0f;
     if constexpr (LMODE == LM_F32) {
+      // Stage 0 is stored as 0 + v (the reference's zero-initialised sum).
+      const float z = s == 0 ? 0.0f : -0.0f;
       u32x4_t a, b;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        a[j] = __float_as_uint(has_ss ? v[j] * ss : v[j]);
-        b[j] = __float_as_uint(has_ss ? v[4 + j] * ss : v[4 + j]);
+        a[j] = __float_as_uint(z + (has_ss ? v[j] * ss : v[j]));
+        b[j] = __float_as_uint(z + (has_ss ? v[4 + j] * ss : v[4 + j]));
       }
       u32x4_t* dst = reinterpret_cast<u32x4_t*>(lds + (size_t)e * 32);
       dst[0] = a;
@@ -147,8 +161,8 @@ __device__ inline u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S]
 #pragma unroll
     for (int pr = 0; pr < 4; ++pr) {
       const int h = pr >> 1, o = (pr & 1) * 2;
-      float tl = 0.0f + __uint_as_float(c[0][h][o]);
-      float th = 0.0f + __uint_as_float(c[0][h][o + 1]);
+      float tl = __uint_as_float(c[0][h][o]);  // staged as 0 + v
+      float th = __uint_as_float(c[0][h][o + 1]);
 #pragma unroll
       for (int s = 1; s < S; ++s) {
         tl = tl + __uint_as_float(c[s][h][o]);
@@ -161,6 +175,8 @@ __device__ inline u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S]
 #pragma unroll
     for (int s = 0; s < S; ++s) c[s] = *reinterpret_cast<const u32x4_t*>(lds + ((size_t)s * K + id[s]) * 16);
     if constexpr (LMODE == LM_H16) {
+      // stage 0 is staged as 0 + v, so c0 + c1 + ... equals the reference's
+      // ((0 + c0) + c1) + ... bit for bit, signed zeros included
 #pragma unroll
       for (int pr = 0; pr < 4; ++pr) {
         float tl = mix_add_lo(c[0][pr], c[1][pr]);
