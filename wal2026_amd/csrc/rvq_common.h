@@ -22,6 +22,11 @@
 
 #include "wal2026_amd.h"
 
+// Device helpers are force-inlined: a call boundary turns LDS pointers into
+// flat pointers and by-value structs into stack traffic.
+#define WAL_DEVICE __device__ __attribute__((always_inline)) inline
+#define WAL_HOST_DEVICE __host__ __device__ __attribute__((always_inline)) inline
+
 namespace wal {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -30,6 +35,19 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4_t g_u32x4_t;
+
+// 128-bit loads from the global address space.  Buffers reach the kernels as
+// plain (flat) pointers; a flat load may alias LDS, which serialises it
+// against LDS stores and makes every LDS wait also wait for it.  Casting to
+// address space 1 gives global_load instructions with their own counter.
+WAL_DEVICE u32x4_t ldg128(const void* p) { return *(g_u32x4_t*)(p); }
+// Streaming variant (non-temporal): data read exactly once, kept out of the
+// way of the small tables and activations that are reused.
+WAL_DEVICE u32x4_t ldg128_stream(const void* p) { return __builtin_nontemporal_load((g_u32x4_t*)(p)); }
+// Scalar element of a global buffer.
+template <typename T>
+WAL_DEVICE T ldg(const void* p, int64_t i) { return ((const __attribute__((address_space(1))) T*)(p))[i]; }
 
 // ---------------------------------------------------------------------------
 // Plan image (built on the host by wal_rvq_plan_build, read by kernels).
@@ -80,7 +98,7 @@ struct TileInfo {
   int32_t out_row0;  // first output row
 };
 
-__device__ inline TileInfo get_tile(const LayerArgs& L, int t) {
+WAL_DEVICE TileInfo get_tile(const LayerArgs& L, int t) {
   TileInfo ti;
   if (L.plan == nullptr) {
     ti.g = L.g0;
@@ -89,15 +107,28 @@ __device__ inline TileInfo get_tile(const LayerArgs& L, int t) {
     ti.rows = min(L.tile_rows, L.g0.rows - ti.row0);
     ti.out_row0 = L.g0.row0 + ti.row0;
   } else {
-    const char* base = reinterpret_cast<const char*>(L.plan);
-    const PlanTile* tiles = reinterpret_cast<const PlanTile*>(base + L.plan->tiles_offset[L.tile_kind]);
-    const wal_rvq_group* groups = reinterpret_cast<const wal_rvq_group*>(base + L.plan->groups_offset);
-    PlanTile pt = tiles[t];
-    ti.g = groups[pt.group];
-    ti.group = pt.group;
-    ti.row0 = pt.row0;
-    ti.rows = pt.rows;
-    ti.out_row0 = pt.out_row0;
+    typedef const __attribute__((address_space(1))) PlanHeader g_header_t;
+    typedef const __attribute__((address_space(1))) PlanTile g_tile_t;
+    typedef const __attribute__((address_space(1))) wal_rvq_group g_group_t;
+    const __attribute__((address_space(1))) char* base = (const __attribute__((address_space(1))) char*)(L.plan);
+    g_header_t* H = (g_header_t*)base;
+    g_tile_t* tiles = (g_tile_t*)(base + H->tiles_offset[L.tile_kind]);
+    g_group_t* groups = (g_group_t*)(base + H->groups_offset);
+    g_tile_t* pt = tiles + t;
+    g_group_t* G = groups + pt->group;
+    for (int s = 0; s < WAL_RVQ_MAX_STAGES; ++s) {
+      ti.g.stage_ids[s] = G->stage_ids[s];
+      ti.g.codebooks[s] = G->codebooks[s];
+    }
+    ti.g.stage_scales = G->stage_scales;
+    ti.g.row_scale = G->row_scale;
+    ti.g.block_scale = G->block_scale;
+    ti.g.row0 = G->row0;
+    ti.g.rows = G->rows;
+    ti.group = pt->group;
+    ti.row0 = pt->row0;
+    ti.rows = pt->rows;
+    ti.out_row0 = pt->out_row0;
   }
   return ti;
 }
@@ -105,14 +136,14 @@ __device__ inline TileInfo get_tile(const LayerArgs& L, int t) {
 // ---------------------------------------------------------------------------
 // Scalar conversions.
 // ---------------------------------------------------------------------------
-__device__ inline float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+WAL_DEVICE float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-__device__ inline float f16_to_f32(uint32_t h) {
+WAL_DEVICE float f16_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
 // fp32 -> bf16 round-to-nearest-even; NaN -> 0x7fc0 (torch's scalar rule).
-__device__ inline uint32_t f32_to_bf16_rne(float f) {
+WAL_DEVICE uint32_t f32_to_bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
@@ -120,7 +151,7 @@ __device__ inline uint32_t f32_to_bf16_rne(float f) {
 
 // fp32 -> fp16 round-to-nearest-even, subnormals and overflow per IEEE-754;
 // NaN -> sign | 0x7e00 (torch's scalar rule).
-__device__ inline uint32_t f32_to_f16_rne(float f) {
+WAL_DEVICE uint32_t f32_to_f16_rne(float f) {
   uint32_t u = __float_as_uint(f);
   uint32_t sign = (u >> 16) & 0x8000u;
   uint32_t a = u & 0x7fffffffu;
@@ -145,65 +176,65 @@ __device__ inline uint32_t f32_to_f16_rne(float f) {
 }
 
 template <int DT>
-__device__ inline float round_dt(float v) {
+WAL_DEVICE float round_dt(float v) {
   if constexpr (DT == WAL_BF16) return bf16_to_f32(f32_to_bf16_rne(v));
   else if constexpr (DT == WAL_F16) return f16_to_f32(f32_to_f16_rne(v));
   else return v;
 }
 
 template <int DT>
-__device__ inline uint32_t to_bits16(float v) {
+WAL_DEVICE uint32_t to_bits16(float v) {
   if constexpr (DT == WAL_BF16) return f32_to_bf16_rne(v);
   else return f32_to_f16_rne(v);
 }
 
 // Load element i of a float buffer of runtime dtype dt as fp32 (exact).
-__device__ inline float load_f(const void* p, int dt, int64_t i) {
-  if (dt == WAL_F16) return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
-  if (dt == WAL_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
-  return reinterpret_cast<const float*>(p)[i];
+WAL_DEVICE float load_f(const void* p, int dt, int64_t i) {
+  if (dt == WAL_F16) return f16_to_f32(ldg<uint16_t>(p, i));
+  if (dt == WAL_BF16) return bf16_to_f32(ldg<uint16_t>(p, i));
+  return ldg<float>(p, i);
 }
 
-__device__ inline int64_t load_id(const void* p, int dt, int64_t i) {
-  if (dt == WAL_U8) return reinterpret_cast<const uint8_t*>(p)[i];
-  if (dt == WAL_I16) return reinterpret_cast<const int16_t*>(p)[i];
-  if (dt == WAL_U16) return reinterpret_cast<const uint16_t*>(p)[i];
-  return reinterpret_cast<const int32_t*>(p)[i];
+WAL_DEVICE int64_t load_id(const void* p, int dt, int64_t i) {
+  if (dt == WAL_U8) return ldg<uint8_t>(p, i);
+  if (dt == WAL_I16) return ldg<int16_t>(p, i);
+  if (dt == WAL_U16) return ldg<uint16_t>(p, i);
+  return ldg<int32_t>(p, i);
 }
 
 // Hardware packed conversions (round-to-nearest-even for finite inputs).
-__device__ inline uint32_t pack_bf16(float lo, float hi) {
+WAL_DEVICE uint32_t pack_bf16(float lo, float hi) {
   bf16x2_t r = {(__bf16)lo, (__bf16)hi};
   return __builtin_bit_cast(uint32_t, r);
 }
-__device__ inline uint32_t pack_f16(float lo, float hi) {
+WAL_DEVICE uint32_t pack_f16(float lo, float hi) {
   f16x2_t r = {(_Float16)lo, (_Float16)hi};
   return __builtin_bit_cast(uint32_t, r);
 }
-__device__ inline float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
-__device__ inline float hi_bf16(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
-__device__ inline float lo_f16(uint32_t p) { return f16_to_f32(p & 0xffffu); }
-__device__ inline float hi_f16(uint32_t p) { return f16_to_f32(p >> 16); }
+WAL_DEVICE float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
+WAL_DEVICE float hi_bf16(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+WAL_DEVICE float lo_f16(uint32_t p) { return f16_to_f32(p & 0xffffu); }
+WAL_DEVICE float hi_f16(uint32_t p) { return f16_to_f32(p >> 16); }
 
 // f32(a.lo) + f32(b.lo) / f32(a.hi) + f32(b.hi) for packed fp16 pairs: one
 // v_fma_mix_f32 each (a * 1.0 + b, a single fp32 rounding == the fp32 add).
-__device__ inline float mix_add_lo(uint32_t a, uint32_t b) {
+WAL_DEVICE float mix_add_lo(uint32_t a, uint32_t b) {
   float r;
   asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
-__device__ inline float mix_add_hi(uint32_t a, uint32_t b) {
+WAL_DEVICE float mix_add_hi(uint32_t a, uint32_t b) {
   float r;
   asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
 // t + f32(a.lo) / t + f32(a.hi) for an fp32 t and a packed fp16 pair.
-__device__ inline float mix_acc_lo(float t, uint32_t a) {
+WAL_DEVICE float mix_acc_lo(float t, uint32_t a) {
   float r;
   asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(a), "v"(t));
   return r;
 }
-__device__ inline float mix_acc_hi(float t, uint32_t a) {
+WAL_DEVICE float mix_acc_hi(float t, uint32_t a) {
   float r;
   asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(a), "v"(t));
   return r;

@@ -20,52 +20,100 @@ namespace wal {
 template <int LMODE>
 __host__ __device__ constexpr int lds_entry_bytes() { return LMODE == LM_F32 ? 32 : 16; }
 
-// Fill LDS with the codebooks of group g (all threads of the block take part).
-template <int S, int LMODE, int SEM, int XDT>
-__device__ inline void stage_codebooks(uint8_t* lds, const wal_rvq_group& g, int K, const DtypeArgs& D) {
-  const int total = S * K;
-  for (int e = threadIdx.x; e < total; e += blockDim.x) {
-    const int s = e / K;
-    const int k = e - s * K;
-    const void* cb = nullptr;
+// The buffers of one row group that the fragment kernels read, with the stage
+// count fixed at compile time so every per-stage pointer has a static index.
+template <int S>
+struct GroupPtrs {
+  const void* ids[S];
+  const void* cb[S];
+  const void* row_scale;
+  const void* stage_scales;
+};
+
+template <int S>
+struct FragTile {
+  GroupPtrs<S> p;
+  int32_t group;
+  int32_t row0;      // first row inside the group
+  int32_t rows;
+  int32_t out_row0;  // first output row
+};
+
+template <int S>
+WAL_DEVICE FragTile<S> get_frag_tile(const LayerArgs& L, int t) {
+  FragTile<S> f;
+  if (L.plan == nullptr) {
 #pragma unroll
-    for (int ss = 0; ss < S; ++ss)
-      if (ss == s) cb = g.codebooks[ss];
-    float v[8];
-    if (D.cb_dtype == WAL_F32) {
-      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(reinterpret_cast<const float*>(cb) + (int64_t)k * 8);
-      u32x4_t a = p[0], b = p[1];
+    for (int s = 0; s < S; ++s) {
+      f.p.ids[s] = L.g0.stage_ids[s];
+      f.p.cb[s] = L.g0.codebooks[s];
+    }
+    f.p.row_scale = L.g0.row_scale;
+    f.p.stage_scales = L.g0.stage_scales;
+    f.group = 0;
+    f.row0 = t * L.tile_rows;
+    f.rows = min(L.tile_rows, L.g0.rows - f.row0);
+    f.out_row0 = L.g0.row0 + f.row0;
+  } else {
+    typedef const __attribute__((address_space(1))) PlanHeader g_header_t;
+    typedef const __attribute__((address_space(1))) PlanTile g_tile_t;
+    typedef const __attribute__((address_space(1))) wal_rvq_group g_group_t;
+    const __attribute__((address_space(1))) char* base = (const __attribute__((address_space(1))) char*)(L.plan);
+    g_header_t* H = (g_header_t*)base;
+    g_tile_t* tiles = (g_tile_t*)(base + H->tiles_offset[L.tile_kind]);
+    g_tile_t* pt = tiles + t;
+    g_group_t* G = (g_group_t*)(base + H->groups_offset) + pt->group;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) { v[j] = __uint_as_float(a[j]); v[4 + j] = __uint_as_float(b[j]); }
-    } else {
-      u32x4_t a = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(cb) + (int64_t)k * 8);
-      if (LMODE == LM_H16) {
-        // fp16 copy.  Stage 0 is stored as 0 + v (-0 becomes +0), the first
-        // add of the reference's zero-initialised fp32 sum, so the fragment
-        // code can sum the stages without a leading zero.
-        if (s == 0) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            uint32_t w = a[j];
-            if ((w & 0xffffu) == 0x8000u) w &= 0xffff0000u;
-            if ((w >> 16) == 0x8000u) w &= 0x0000ffffu;
-            a[j] = w;
-          }
-        }
-        *reinterpret_cast<u32x4_t*>(lds + (size_t)e * 16) = a;
-        continue;
-      }
+    for (int s = 0; s < S; ++s) {
+      f.p.ids[s] = G->stage_ids[s];
+      f.p.cb[s] = G->codebooks[s];
+    }
+    f.p.row_scale = G->row_scale;
+    f.p.stage_scales = G->stage_scales;
+    f.group = pt->group;
+    f.row0 = pt->row0;
+    f.rows = pt->rows;
+    f.out_row0 = pt->out_row0;
+  }
+  return f;
+}
+
+// Convert one raw codebook entry (8 values; fp32 codebooks use both halves of
+// raw) of stage s into its LDS form at entry e.
+template <int LMODE, int SEM, int XDT>
+WAL_DEVICE void store_codebook_entry(uint8_t* lds, int e, int s, const u32x4_t (&raw)[2], int cb_dtype,
+                                            bool has_ss, float ss) {
+  if constexpr (LMODE == LM_H16) {
+    // fp16 copy.  Stage 0 is stored as 0 + v (-0 becomes +0), the first add
+    // of the reference's zero-initialised fp32 sum, so the fragment code can
+    // sum the stages without a leading zero.
+    u32x4_t a = raw[0];
+    if (s == 0) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t w = a[j];
-        if (D.cb_dtype == WAL_F16) { v[2 * j] = f16_to_f32(w & 0xffffu); v[2 * j + 1] = f16_to_f32(w >> 16); }
+        uint32_t w = a[j];
+        if ((w & 0xffffu) == 0x8000u) w &= 0xffff0000u;
+        if ((w >> 16) == 0x8000u) w &= 0x0000ffffu;
+        a[j] = w;
+      }
+    }
+    *reinterpret_cast<u32x4_t*>(lds + (size_t)e * 16) = a;
+  } else {
+    float v[8];
+    if (cb_dtype == WAL_F32) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { v[j] = __uint_as_float(raw[0][j]); v[4 + j] = __uint_as_float(raw[1][j]); }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t w = raw[0][j];
+        if (cb_dtype == WAL_F16) { v[2 * j] = f16_to_f32(w & 0xffffu); v[2 * j + 1] = f16_to_f32(w >> 16); }
         else { v[2 * j] = bf16_to_f32(w & 0xffffu); v[2 * j + 1] = bf16_to_f32(w >> 16); }
       }
     }
-    const bool has_ss = g.stage_scales != nullptr;
-    const float ss = has_ss ? load_f(g.stage_scales, D.sc_dtype, s) : 1.0f;
     if constexpr (LMODE == LM_F32) {
-      // Stage 0 is stored as 0 + v (the reference's zero-initialised sum).
+      // Stage 0 is stored as 0 + v (the reference's zero-initialised sum);
+      // -0 + u == u for every u, so other stages are stored unchanged.
       const float z = s == 0 ? 0.0f : -0.0f;
       u32x4_t a, b;
 #pragma unroll
@@ -76,7 +124,7 @@ __device__ inline void stage_codebooks(uint8_t* lds, const wal_rvq_group& g, int
       u32x4_t* dst = reinterpret_cast<u32x4_t*>(lds + (size_t)e * 32);
       dst[0] = a;
       dst[1] = b;
-    } else if constexpr (LMODE == LM_A16) {
+    } else {  // LM_A16
       u32x4_t o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -100,56 +148,148 @@ __device__ inline void stage_codebooks(uint8_t* lds, const wal_rvq_group& g, int
   }
 }
 
-// Row-scale operand: rf = rne_x(row_scale) as fp32; r2 = that value as a
-// packed fp16 pair (used only when x is fp16).
+// Fill LDS with the codebooks of one group (all threads of the block take
+// part).  16-bit codebooks: each thread issues the loads of 8 entries (over
+// the stages) before converting and storing any, so the load latency is paid
+// once per batch.  fp32 codebooks (rare) take a plain loop.
+template <int S, int LMODE, int SEM, int XDT>
+WAL_DEVICE void stage_codebooks(uint8_t* lds, const GroupPtrs<S>& g, int K, const DtypeArgs& D) {
+  constexpr int U = S >= 8 ? 1 : 8 / S;  // entries per stage per batch
+  const int nt = blockDim.x;
+  const bool has_ss = g.stage_scales != nullptr;
+  float ssv[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) ssv[s] = has_ss ? load_f(g.stage_scales, D.sc_dtype, s) : 1.0f;
+  if (D.cb_dtype == WAL_F32) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const char* cb = static_cast<const char*>(g.cb[s]);
+      for (int k = threadIdx.x; k < K; k += nt) {
+        const u32x4_t raw[2] = {ldg128(cb + (size_t)k * 32), ldg128(cb + (size_t)k * 32 + 16)};
+        store_codebook_entry<LMODE, SEM, XDT>(lds, s * K + k, s, raw, WAL_F32, has_ss, ssv[s]);
+      }
+    }
+    return;
+  }
+  for (int k0 = threadIdx.x; k0 < K; k0 += U * nt) {
+    u32x4_t raw[S][U];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const char* cb = static_cast<const char*>(g.cb[s]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = k0 + u * nt;
+        raw[s][u] = k < K ? ldg128(cb + (size_t)k * 16) : u32x4_t{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = k0 + u * nt;
+        if (k < K) {
+          const u32x4_t r2[2] = {raw[s][u], u32x4_t{0, 0, 0, 0}};
+          store_codebook_entry<LMODE, SEM, XDT>(lds, s * K + k, s, r2, D.cb_dtype, has_ss, ssv[s]);
+        }
+      }
+  }
+}
+
+// Row-scale operand: rf = rne_x(row_scale) as fp32.  For fp16 x, r2 is that
+// value as a packed fp16 pair; for bf16 x, r2 = (rf, 0) and r3 = (0, rf) as
+// packed bf16 pairs, the second operands of v_dot2_f32_bf16 below.
 struct RowScale {
   float rf;
   uint32_t r2;
+  uint32_t r3;
 };
 
 template <int XDT>
-__device__ inline RowScale make_row_scale(float rs) {
+WAL_DEVICE RowScale make_row_scale(float rs) {
   RowScale r;
   r.rf = round_dt<XDT>(rs);
   if constexpr (XDT == WAL_F16) {
     const uint32_t h = f32_to_f16_rne(rs);
     r.r2 = h | (h << 16);
+    r.r3 = 0;
   } else {
-    r.r2 = 0;
+    const uint32_t h = f32_to_bf16_rne(rs);
+    r.r2 = h;
+    r.r3 = h << 16;
   }
   return r;
 }
 
-__device__ inline uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
+WAL_DEVICE uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
   f16x2_t r = __builtin_bit_cast(f16x2_t, a) * __builtin_bit_cast(f16x2_t, b);
   return __builtin_bit_cast(uint32_t, r);
 }
-__device__ inline uint32_t pk_add_f16(uint32_t a, uint32_t b) {
+WAL_DEVICE uint32_t pk_add_f16(uint32_t a, uint32_t b) {
   f16x2_t r = __builtin_bit_cast(f16x2_t, a) + __builtin_bit_cast(f16x2_t, b);
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// rne_x(a * rf) for a packed pair a of x-dtype values.
+// rne_bf16(a_i * s) for the 8 bf16 values a of one fragment (4 packed pairs),
+// s = rne_bf16(row_scale): per pair, v_dot2_f32_bf16 against (s, 0) and
+// (0, s) gives the exact fp32 products a.lo * s and a.hi * s (a product of two
+// bf16 values has at most 16 significant bits; the other term is +-0 and the
+// addend 0, so only the sign of a zero product can differ from a plain
+// multiply, which no fp32 sum that starts at +0 can observe), and
+// v_cvt_pk_bf16_f32 rounds the pair to nearest-even.  Finite inputs only.
+//
+// One asm block: a dot result must be three wait states old before a VALU
+// reads it, which the compiler cannot see through inline asm.  The order
+// below leaves at least three instructions between each dot and the pack
+// that reads it; the closing s_nop gives the two wait states a VALU result
+// needs before an MFMA reads it.
+WAL_DEVICE u32x4_t scale_frag_bf16(const u32x4_t& a, uint32_t slo, uint32_t shi) {
+  u32x4_t w;
+  float t0, t1, t2, t3, t4, t5, t6, t7;
+  asm("v_dot2_f32_bf16 %4, %12, %16, 0\n\t"
+      "v_dot2_f32_bf16 %5, %12, %17, 0\n\t"
+      "v_dot2_f32_bf16 %6, %13, %16, 0\n\t"
+      "v_dot2_f32_bf16 %7, %13, %17, 0\n\t"
+      "v_dot2_f32_bf16 %8, %14, %16, 0\n\t"
+      "v_dot2_f32_bf16 %9, %14, %17, 0\n\t"
+      "v_dot2_f32_bf16 %10, %15, %16, 0\n\t"
+      "v_dot2_f32_bf16 %11, %15, %17, 0\n\t"
+      "v_cvt_pk_bf16_f32 %0, %4, %5\n\t"
+      "v_cvt_pk_bf16_f32 %1, %6, %7\n\t"
+      "v_cvt_pk_bf16_f32 %2, %8, %9\n\t"
+      "v_cvt_pk_bf16_f32 %3, %10, %11\n\t"
+      "s_nop 1"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3),
+        "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(slo), "v"(shi));
+  return w;
+}
+
+// rne_x(a * rf) for the 8 x-dtype values of a fragment (finite).
 template <int XDT>
-__device__ inline uint32_t scale_pair(uint32_t a, const RowScale& rs) {
+WAL_DEVICE u32x4_t scale_frag(const u32x4_t& a, const RowScale& rs) {
   if constexpr (XDT == WAL_F16) {
-    return pk_mul_f16(a, rs.r2);
+    u32x4_t w;
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) w[pr] = pk_mul_f16(a[pr], rs.r2);
+    return w;
   } else {
-    return pack_bf16(lo_bf16(a) * rs.rf, hi_bf16(a) * rs.rf);
+    return scale_frag_bf16(a, rs.r2, rs.r3);
   }
 }
 
 template <int XDT>
-__device__ inline uint32_t pack_x(float lo, float hi) {
+WAL_DEVICE uint32_t pack_x(float lo, float hi) {
   if constexpr (XDT == WAL_F16) return pack_f16(lo, hi);
   else return pack_bf16(lo, hi);
 }
 
-// 8-weight fragment for stage ids id[0..S-1].
+// 8-weight fragment for stage ids id[0..S-1]: the pre-scale values in x
+// dtype (RECON: rne_x of the fp32 stage sum; FAST: the x-dtype stage sum),
+// then the row-scale product.
 template <int S, int LMODE, int SEM, int XDT>
-__device__ inline u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S], int K, uint32_t active,
-                                     const RowScale& rs) {
-  u32x4_t w;
+WAL_DEVICE u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S], int K, uint32_t active,
+                              const RowScale& rs) {
+  u32x4_t a;
   if constexpr (LMODE == LM_F32) {
     u32x4_t c[S][2];
 #pragma unroll
@@ -168,7 +308,7 @@ __device__ inline u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S]
         tl = tl + __uint_as_float(c[s][h][o]);
         th = th + __uint_as_float(c[s][h][o + 1]);
       }
-      w[pr] = scale_pair<XDT>(pack_x<XDT>(tl, th), rs);
+      a[pr] = pack_x<XDT>(tl, th);
     }
   } else {
     u32x4_t c[S];
@@ -186,37 +326,36 @@ __device__ inline u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S]
           tl = mix_acc_lo(tl, c[s][pr]);
           th = mix_acc_hi(th, c[s][pr]);
         }
-        w[pr] = scale_pair<XDT>(pack_x<XDT>(tl, th), rs);
+        a[pr] = pack_x<XDT>(tl, th);
       }
     } else if constexpr (SEM == SEM_RECON) {  // LM_A16, S == 1
-#pragma unroll
-      for (int pr = 0; pr < 4; ++pr) w[pr] = scale_pair<XDT>(c[0][pr], rs);
+      a = c[0];
     } else {  // LM_A16, FAST
 #pragma unroll
       for (int pr = 0; pr < 4; ++pr) {
-        uint32_t a = 0;
+        uint32_t v = 0;
         bool first = true;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           if (!(active & (1u << s))) continue;
           if (first) {
-            a = c[s][pr];
+            v = c[s][pr];
             first = false;
           } else if constexpr (XDT == WAL_F16) {
-            a = pk_add_f16(a, c[s][pr]);
+            v = pk_add_f16(v, c[s][pr]);
           } else {
-            a = pack_bf16(lo_bf16(a) + lo_bf16(c[s][pr]), hi_bf16(a) + hi_bf16(c[s][pr]));
+            v = pack_bf16(lo_bf16(v) + lo_bf16(c[s][pr]), hi_bf16(v) + hi_bf16(c[s][pr]));
           }
         }
-        w[pr] = scale_pair<XDT>(a, rs);
+        a[pr] = v;
       }
     }
   }
-  return w;
+  return scale_frag<XDT>(a, rs);
 }
 
 template <int XDT>
-__device__ inline f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+WAL_DEVICE f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
   if constexpr (XDT == WAL_F16) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
                                                   0, 0, 0);

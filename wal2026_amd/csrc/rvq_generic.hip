@@ -14,12 +14,12 @@ namespace wal {
 // Index clamped into [0, K): ids are validated by the host when a plan is
 // built; the clamp keeps a corrupt index from ever becoming a load outside the
 // codebook.
-__device__ inline int64_t clamp_id(int64_t id, int K) { return id < 0 ? 0 : (id >= K ? K - 1 : id); }
+WAL_DEVICE int64_t clamp_id(int64_t id, int K) { return id < 0 ? 0 : (id >= K ? K - 1 : id); }
 
 // One weight element W[r, col] of a group (r = row inside the group) as fp32
 // holding a value exact in DT.  rs is row_scale[r] as fp32 (exact).
 template <int SEM, int DT>
-__device__ inline float weight_elem(const LayerArgs& L, const wal_rvq_group& g, const DtypeArgs& D,
+WAL_DEVICE float weight_elem(const LayerArgs& L, const wal_rvq_group& g, const DtypeArgs& D,
                                     int64_t r, int col, float rs) {
   if constexpr (SEM == SEM_ROUTE0 || SEM == SEM_ROUTE1) {
     // ids [rows, in_features] (d = 1, one stage), codebook_sum in codebooks[0].
@@ -74,7 +74,7 @@ __device__ inline float weight_elem(const LayerArgs& L, const wal_rvq_group& g, 
 }
 
 template <int DT>
-__device__ inline void store_elem(void* out, int64_t i, float v) {
+WAL_DEVICE void store_elem(void* out, int64_t i, float v) {
   if constexpr (DT == WAL_F32) reinterpret_cast<float*>(out)[i] = v;
   else reinterpret_cast<uint16_t*>(out)[i] = (uint16_t)to_bits16<DT>(v);
 }

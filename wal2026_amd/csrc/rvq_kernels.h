@@ -35,13 +35,13 @@ struct EpilogueArgs {
   int32_t bias_mode;
 };
 
-__device__ inline float round_rt(float v, int dt) {
+WAL_DEVICE float round_rt(float v, int dt) {
   if (dt == WAL_BF16) return round_dt<WAL_BF16>(v);
   if (dt == WAL_F16) return round_dt<WAL_F16>(v);
   return v;
 }
 
-__device__ inline void store_output(const EpilogueArgs& E, int64_t m, int64_t n, float acc) {
+WAL_DEVICE void store_output(const EpilogueArgs& E, int64_t m, int64_t n, float acc) {
   float v = acc;
   if (E.bias_mode != 0) {
     const float b = round_rt(load_f(E.bias, E.bias_dtype, n), E.x_dtype);
@@ -69,6 +69,26 @@ hipError_t decode_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueAr
 template <int XDT, typename IdT>
 hipError_t prefill_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
                          const void* x, int64_t M, hipStream_t st);
+
+// One explicit instantiation per (activation dtype, index width), each in its
+// own translation unit (rvq_decode_<x>_<ids>.hip, rvq_prefill_<x>_<ids>.hip);
+// these declarations keep every other unit from instantiating them again.
+extern template hipError_t decode_entry<WAL_BF16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
+                                                           int, int, const void*, int, int, hipStream_t);
+extern template hipError_t decode_entry<WAL_BF16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
+                                                            int, int, const void*, int, int, hipStream_t);
+extern template hipError_t decode_entry<WAL_F16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
+                                                          int, int, const void*, int, int, hipStream_t);
+extern template hipError_t decode_entry<WAL_F16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
+                                                           int, int, const void*, int, int, hipStream_t);
+extern template hipError_t prefill_entry<WAL_BF16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
+                                                            int, int, const void*, int64_t, hipStream_t);
+extern template hipError_t prefill_entry<WAL_BF16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
+                                                             int, int, const void*, int64_t, hipStream_t);
+extern template hipError_t prefill_entry<WAL_F16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
+                                                           int, int, const void*, int64_t, hipStream_t);
+extern template hipError_t prefill_entry<WAL_F16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
+                                                            int, int, const void*, int64_t, hipStream_t);
 
 inline hipError_t launch_decode(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
                                 int lds_mode, const void* x, int M, int n_cu, hipStream_t st) {

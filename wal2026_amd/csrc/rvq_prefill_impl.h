@@ -35,14 +35,14 @@ __global__ __launch_bounds__(256) void rvq_prefill_kernel(LayerArgs L, DtypeArgs
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int l16 = lane & 15, q = lane >> 4;
-  const TileInfo ti = get_tile(L, blockIdx.x);
+  const FragTile<S> ti = get_frag_tile<S>(L, blockIdx.x);
   const int64_t m0 = (int64_t)blockIdx.y * PM;
   const int B = L.blocks_per_row;
   const int in = L.in_features;
   const int nk = (in + PK - 1) / PK;
   const uint32_t kmax = (uint32_t)(K - 1);
 
-  stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, ti.g, K, D);
+  stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, ti.p, K, D);
 
   // loader roles: row lr = tid / 2, half lh = tid % 2
   const int lr = tid >> 1, lh = tid & 1;
@@ -51,11 +51,11 @@ __global__ __launch_bounds__(256) void rvq_prefill_kernel(LayerArgs L, DtypeArgs
   const uint16_t* xrow = x + xm * in;
   const bool w_row_ok = lr < ti.rows;
   const int64_t wr = ti.row0 + lr;
-  const float rs_raw = w_row_ok ? load_f(ti.g.row_scale, D.sc_dtype, wr / L.scale_rows) : 0.0f;
+  const float rs_raw = w_row_ok ? load_f(ti.p.row_scale, D.sc_dtype, wr / L.scale_rows) : 0.0f;
   const RowScale rs = make_row_scale<XDT>(rs_raw);
   const IdT* idp[S];
 #pragma unroll
-  for (int s = 0; s < S; ++s) idp[s] = reinterpret_cast<const IdT*>(ti.g.stage_ids[s]) + wr * B;
+  for (int s = 0; s < S; ++s) idp[s] = reinterpret_cast<const IdT*>(ti.p.ids[s]) + wr * B;
 
   u32x4_t xreg[4];
   uint32_t idreg[S][4];
@@ -65,14 +65,14 @@ __global__ __launch_bounds__(256) void rvq_prefill_kernel(LayerArgs L, DtypeArgs
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int col = col0 + 8 * i;
-      xreg[i] = (x_row_ok && col < in) ? *reinterpret_cast<const u32x4_t*>(xrow + col) : u32x4_t{0, 0, 0, 0};
+      xreg[i] = (x_row_ok && col < in) ? ldg128(xrow + col) : u32x4_t{0, 0, 0, 0};
     }
     const int b0 = k * (PK / 8) + 4 * lh;
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        idreg[s][i] = (w_row_ok && b0 + i < B) ? (uint32_t)idp[s][b0 + i] : 0u;
+        idreg[s][i] = (w_row_ok && b0 + i < B) ? (uint32_t)ldg<IdT>(idp[s], b0 + i) : 0u;
   };
   auto store_step = [&](int k, int bufi) {
     uint16_t* xd = xs + bufi * kTileElems + lr * PSTRIDE + 32 * lh;
