@@ -60,12 +60,18 @@ def linear_bytes(cfg: synth.Config, n: int, k: int) -> int:
 
 
 def time_kernel_family(stack, name, x, reps: int = 3) -> float:
-    """Average duration (us) of one launch of `name`, from a HIP event pair
-    around every launch, cycling through all layers so each launch reads
-    weights not touched by the previous ones."""
+    """Average GPU duration (us) of one launch of `name`.
+
+    The launches (one per layer, so each reads weights the previous one did
+    not) are queued behind a GPU sleep, so the host enqueues all of them before
+    the first runs and the HIP event pair recorded around each launch on the
+    launching stream brackets that kernel's own execution, not host latency.
+    """
     stream = torch.cuda.current_stream()
     times = []
     for _ in range(reps):
+        torch.cuda.synchronize()
+        torch.cuda._sleep(20_000_000)  # ~10 ms of GPU spin: the queue fills behind it
         pairs = []
         for layer in stack:
             a = torch.cuda.Event(enable_timing=True)

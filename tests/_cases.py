@@ -13,7 +13,9 @@ def make_encoding(out_features: int, in_features: int, *, d: int = 8, S: int = 2
                   cb_dtype: torch.dtype = torch.float16, stage_scales: bool = False, block_scale: bool = False,
                   stages_per_split: tuple[int, ...] | None = None, product_splits: int = 1,
                   special: bool = False, seed: int = 0, scale_dtype: torch.dtype = torch.float16,
-                  ) -> GroupedBlockRVQEncoding:
+                  scale_run: int | None = None) -> GroupedBlockRVQEncoding:
+    """scale_run: rows of a group share their row scale in aligned runs of
+    that many rows (a per-row-group scale expanded to rows)."""
     g = torch.Generator().manual_seed(seed)
     id_dtype = id_dtype or _id_storage_dtype(K)
     B = -(-in_features // d)
@@ -44,6 +46,8 @@ def make_encoding(out_features: int, in_features: int, *, d: int = 8, S: int = 2
         rs = (torch.rand(rows, 1, generator=g) + 0.5)
         if special:
             rs[: max(rows // 8, 1)] = torch.randint(1, 64, (max(rows // 8, 1), 1), generator=g).float() * 2.0 ** -6
+        if scale_run:
+            rs = rs[::scale_run].repeat_interleave(scale_run, dim=0)[:rows]
         rs = rs.to(scale_dtype)
         ss = (torch.rand(S, generator=g) + 0.5).to(scale_dtype) if stage_scales else None
         bs = (torch.rand(rows, B, generator=g) + 0.5).to(scale_dtype) if block_scale else None

@@ -29,6 +29,10 @@ LAYOUTS = [
     ("c1like_s2_u8", 256, 512, 8, 2, 256, None, None, {}),
     ("s1_k4096_i16", 160, 256, 8, 1, 4096, None, None, {}),
     ("s1_k4096_u16", 64, 128, 8, 1, 4096, torch.uint16, None, {}),
+    # one stage with row scales shared by aligned runs of rows: the decode
+    # kernel stages the codebook already multiplied by the scale
+    ("s1_k4096_u16_scale128", 384, 256, 8, 1, 4096, torch.uint16, None, {"scale_run": 128}),
+    ("s1_k256_scale16_ragged_groups", 200, 384, 8, 1, 256, None, 96, {"scale_run": 16}),
     ("s3_groups256_ragged", 600, 384, 8, 3, 256, None, 256, {}),
     ("s4_u8", 96, 256, 8, 4, 256, None, None, {}),
     ("s2_stage_scales", 128, 256, 8, 2, 256, None, None, {"stage_scales": True}),
@@ -134,6 +138,26 @@ def test_fast_strategy_parity(layout, m, gpu_device):
     else:
         w_ref = oracle_weight(module_buffers_as_encoding(mod), torch.bfloat16)
     assert rel_err(y, c_oracle.linear_f64(x, w_ref)) <= TOL
+
+
+SCALED_LAYOUTS = [l for l in LAYOUTS if l[8].get("scale_run")]
+
+
+@pytest.mark.parametrize("layout", SCALED_LAYOUTS, ids=[l[0] for l in SCALED_LAYOUTS])
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float16], ids=["xbf16", "xf16"])
+def test_scale_runs_detected_and_fast_parity(layout, x_dtype, gpu_device):
+    """Shared row scales are passed to the library as a compact buffer
+    (scale_rows > 1); reconstruct_weight_fast semantics (S = 1) on that path."""
+    mod = _module(layout, gpu_device, matmul_strategy="per_group_fast")
+    assert mod._descriptor().layer.scale_rows >= 16
+    x = torch.randn(3, mod.in_features, generator=torch.Generator().manual_seed(4)).to(x_dtype)
+    y = mod._hip_linear(x.to(gpu_device), fast=True, out_dtype=torch.float32)
+    w_ref = oracle_weight(module_buffers_as_encoding(mod), x_dtype, active=[0])
+    assert rel_err(y, c_oracle.linear_f64(x, w_ref)) <= 1e-5
+    # the decode kernel's weights, read out through one-hot rows, are exact
+    eye = torch.eye(16, mod.in_features, dtype=x_dtype)
+    got = mod._hip_linear(eye.to(gpu_device), fast=True, out_dtype=torch.float32).cpu().t()
+    assert torch.equal(got, w_ref[:, :16].float())
 
 
 @pytest.mark.parametrize("m", [1, 5, 40])

@@ -125,6 +125,7 @@ LayerArgs make_args(const wal_rvq_layer& L, int kind, uint32_t active_mask) {
   A.codebook_size = L.codebook_size;
   A.num_stages = L.num_stages;
   A.scale_rows = L.scale_rows;
+  A.scale_shift = (L.scale_rows & (L.scale_rows - 1)) == 0 ? __builtin_ctz((unsigned)L.scale_rows) : -1;
   A.tile_kind = kind;
   A.tile_rows = kTileRows[kind];
   A.n_tiles = n_tiles_of(L, kind);
@@ -161,15 +162,21 @@ bool mfma_eligible(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, 
   if (L.num_stages > 4) return false;
   if (L.id_dtype == WAL_I32) return false;
   if (!is_half_dtype(x_dtype) || !aligned16(x)) return false;
+  if (!is_half_dtype(L.scale_dtype)) return false;
   for (int g = 0; g < L.n_groups; ++g) {
     const wal_rvq_group& G = L.groups[g];
     if (G.block_scale) return false;
     for (int s = 0; s < L.num_stages; ++s)
       if (!aligned16(G.stage_ids[s]) || !aligned16(G.codebooks[s])) return false;
   }
+  // index and scale buffers are addressed with 32-bit buffer offsets
+  for (int g = 0; g < L.n_groups; ++g)
+    if ((int64_t)L.groups[g].rows * L.blocks_per_row * id_bytes(L.id_dtype) >= (int64_t)1 << 31) return false;
   const int esz = lds_mode_for(L, sem) == LM_F32 ? 32 : 16;
   const size_t cb = (size_t)L.num_stages * L.codebook_size * esz;
-  const size_t budget = prefill ? (160 * 1024 - 4 * 128 * 72 * 2) : (160 * 1024 - 8 * 1024);
+  // prefill: four 128 x 72 16-bit tiles; decode: the partial sums of one
+  // tile from 8 waves at M = 16 and the zero row
+  const size_t budget = prefill ? (160 * 1024 - 4 * 128 * 72 * 2) : (160 * 1024 - 8 * 1024 - 256);
   return cb <= budget;
 }
 

@@ -45,6 +45,21 @@ WAL_DEVICE u32x4_t ldg128(const void* p) { return *(g_u32x4_t*)(p); }
 // Streaming variant (non-temporal): data read exactly once, kept out of the
 // way of the small tables and activations that are reused.
 WAL_DEVICE u32x4_t ldg128_stream(const void* p) { return __builtin_nontemporal_load((g_u32x4_t*)(p)); }
+// Raw buffer loads through a resource descriptor covering [p, p + 2 GiB):
+// an offset at or past kBufOOB is out of range, and the hardware returns
+// zeros without a memory access (used for pipeline slots past the end of the
+// work).  Dword 3 of the descriptor: 32-bit raw data format.
+typedef __amdgpu_buffer_rsrc_t bufrsrc_t;
+constexpr uint32_t kBufOOB = 0x80000000u;
+WAL_DEVICE bufrsrc_t make_rsrc(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)kBufOOB, 0x00020000);
+}
+// 16 bytes at byte offset off, non-temporal (streamed once).
+WAL_DEVICE u32x4_t ldbuf128_stream(bufrsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
+WAL_DEVICE uint32_t ldbuf16(bufrsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
+
 // Scalar element of a global buffer.
 template <typename T>
 WAL_DEVICE T ldg(const void* p, int64_t i) { return ((const __attribute__((address_space(1))) T*)(p))[i]; }
@@ -85,10 +100,16 @@ struct LayerArgs {
   int32_t tile_rows;     // rows per tile for the kernel's tile kind
   int32_t tile_kind;
   uint32_t active_mask;  // RECONSTRUCT_FAST active stages
-  int32_t pad;
+  int32_t scale_shift;   // log2(scale_rows) when it is a power of two, else -1
   const PlanHeader* plan;  // NULL -> single group g0
   wal_rvq_group g0;
 };
+
+// row_scale entry of row r (inside its group): r / scale_rows, a shift when
+// scale_rows is a power of two.
+WAL_HOST_DEVICE int64_t scale_index(const LayerArgs& L, int64_t r) {
+  return L.scale_shift >= 0 ? (r >> L.scale_shift) : r / L.scale_rows;
+}
 
 struct TileInfo {
   wal_rvq_group g;  // by value: no pointer into the kernel-argument segment

@@ -1,40 +1,52 @@
 // rvq_decode_impl.h -- Block-RVQ linear for M <= 16 (decode), block_size 8.
 //
 // The weight is never written to memory.  Layout of the work:
-//   * A workgroup of NW waves is persistent over a contiguous range of
+//   * A workgroup of NW = blockDim.x / 64 waves takes a contiguous range of
 //     16-row tiles.  It keeps the codebooks of the current row group in LDS
 //     (restaged only when the tile's group changes) and, when it fits, the
 //     activation rows x[0..M) as well.
 //   * Within a tile the row's 64-block chunks are dealt to the waves: wave w
 //     takes chunks w, w + NW, ...; every wave takes the same number CPT of
-//     chunk slots per tile (a slot past the last chunk contributes zero), so
-//     the sequence of (tile, slot) items is the same length for every wave
-//     and the per-tile barriers are uniform.
+//     chunk slots per tile (a slot past the last chunk contributes nothing),
+//     so the per-tile barriers are uniform.
 //   * Lane l covers weight row n = l % 16 and the 16 consecutive blocks
 //     [64c + 16q, 64c + 16q + 16), q = l / 16: one 128-bit load per stage for
-//     8-bit ids, two for 16-bit ids.  Those loads run PF items ahead of the
-//     compute, across tile boundaries (a ring of PF register slots).
-//   * For each of the 16 blocks the lane gathers the S codewords from LDS,
-//     rebuilds the 8 weights exactly as the reference's dequantisation does
-//     (rvq_fragment.h) and feeds them as the B operand of
-//     v_mfma_f32_16x16x32_{bf16,f16}; the A operand is x[min(l % 16, M - 1)] at
-//     the same 8 columns (rows m >= M of the product are never stored).
-//   * The NW partial 16x16 accumulators of a tile are summed through LDS and
-//     the M x 16 outputs written once.
+//     8-bit ids, two for 16-bit ids.
+//   * Software pipeline: the index loads (and the lane's row-scale load) of
+//     the item PF slots ahead are issued right after an item is consumed, as
+//     straight-line code into a fixed register ring, so the hardware keeps PF
+//     items of loads in flight per wave and the only memory waits in the loop
+//     are the in-order ones for the slot being consumed.  Loads past the end
+//     of the range are clamped to a valid address and their results unused.
+//     Per-tile metadata comes from the plan through the scalar cache.
+//   * For each block the lane gathers the S codewords from LDS, rebuilds the 8
+//     weights exactly as the reference's dequantisation does (rvq_fragment.h)
+//     and feeds them as the B operand of v_mfma_f32_16x16x32_{bf16,f16}; the A
+//     operand is x[min(l % 16, M - 1)] at the same 8 columns (rows m >= M of
+//     the product are never stored).
+//   * SCALED (one stage, every 16-row tile under a single row-scale value):
+//     the codebook is staged already multiplied by the tile's scale with the
+//     reference's rounding, so the hot loop is gather + MFMA only; the staged
+//     table is rebuilt when the scale changes.
+//   * No barrier and no global store per tile: each wave parks its partial
+//     16x16 accumulator of a tile in LDS; after the last tile of the range the
+//     workgroup sums the NW partials and writes the M x 16 outputs of every
+//     tile.  (A global store pending beside the index loads would make the
+//     compiler's in-order load waits fall back to full drains.)
 #pragma once
 
 #include "rvq_fragment.h"
 
 namespace wal {
 
-constexpr int kDecodeWaves = 4;
-constexpr int kDecodeThreads = kDecodeWaves * 64;
+constexpr int kDecodeMaxWaves = 8;
+constexpr int kDecodeMaxThreads = kDecodeMaxWaves * 64;
 
 // Items of index loads in flight per wave: about 128 bytes per lane.
 template <int S, typename IdT>
 constexpr int decode_prefetch() {
   constexpr int w = S * (int)sizeof(IdT);
-  return w <= 2 ? 4 : (w <= 4 ? 2 : 1);
+  return w <= 1 ? 8 : (w <= 2 ? 4 : (w <= 3 ? 3 : 2));
 }
 
 template <typename IdT>
@@ -46,25 +58,84 @@ WAL_DEVICE uint32_t extract_id(const u32x4_t (&v)[sizeof(IdT)], int t) {
   }
 }
 
-// Bytes of LDS a decode launch needs (codebooks + reduction buffer + x).
+// Bytes of LDS a decode launch needs: codebooks, the per-tile partial sums of
+// every wave (max_tiles tiles per workgroup), a 256-byte zero row and (xlds)
+// the activation rows.
 template <int LMODE>
-WAL_HOST_DEVICE size_t decode_lds_bytes(int S, int K, bool xlds, int M, int in) {
-  return (size_t)S * K * lds_entry_bytes<LMODE>() + 2 * kDecodeWaves * 256 * sizeof(float) +
+WAL_HOST_DEVICE size_t decode_lds_bytes(int S, int K, bool xlds, int M, int in, int nw, int max_tiles) {
+  return (size_t)S * K * lds_entry_bytes<LMODE>() + (size_t)max_tiles * nw * M * 16 * sizeof(float) + 256 +
          (xlds ? (size_t)M * in * sizeof(uint16_t) : 0);
 }
 
-template <int S, typename IdT, int LMODE, int SEM, int XDT, bool XLDS>
-__global__ __launch_bounds__(kDecodeThreads) void rvq_decode_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
-                                                                    const uint16_t* __restrict__ x, int M) {
-  constexpr int NW = kDecodeWaves, PF = decode_prefetch<S, IdT>(), NV = sizeof(IdT);
+// Tile metadata through the scalar cache (uniform t): no vector-memory
+// instruction, so reading it never waits on the index loads in flight.
+template <int S>
+WAL_DEVICE FragTile<S> tile_at(const LayerArgs& L, int t) {
+  FragTile<S> f;
+  if (L.plan == nullptr) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      f.p.ids[s] = L.g0.stage_ids[s];
+      f.p.cb[s] = L.g0.codebooks[s];
+    }
+    f.p.row_scale = L.g0.row_scale;
+    f.p.stage_scales = L.g0.stage_scales;
+    f.group = 0;
+    f.row0 = t * 16;
+    f.rows = min(16, L.g0.rows - f.row0);
+    f.out_row0 = L.g0.row0 + f.row0;
+  } else {
+    typedef const __attribute__((address_space(4))) PlanHeader c_header_t;
+    typedef const __attribute__((address_space(4))) PlanTile c_tile_t;
+    typedef const __attribute__((address_space(4))) wal_rvq_group c_group_t;
+    const __attribute__((address_space(4))) char* base = (const __attribute__((address_space(4))) char*)(L.plan);
+    c_header_t* H = (c_header_t*)base;
+    c_tile_t* pt = (c_tile_t*)(base + H->tiles_offset[0]) + t;
+    c_group_t* G = (c_group_t*)(base + H->groups_offset) + pt->group;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      f.p.ids[s] = G->stage_ids[s];
+      f.p.cb[s] = G->codebooks[s];
+    }
+    f.p.row_scale = G->row_scale;
+    f.p.stage_scales = G->stage_scales;
+    f.group = pt->group;
+    f.row0 = pt->row0;
+    f.rows = pt->rows;
+    f.out_row0 = pt->out_row0;
+  }
+  return f;
+}
+
+WAL_DEVICE float scale_bits_to_f32(uint32_t h, int dt) { return dt == WAL_F16 ? f16_to_f32(h) : bf16_to_f32(h); }
+
+// Where the MFMA's activation fragments come from.
+enum XMode : int {
+  XM_GLOBAL = 0,  // x does not fit in LDS: read per item from global memory (L2)
+  XM_LDS = 1,     // x staged in LDS, fragments read per item
+  XM_REG = 2      // x staged in LDS; each wave owns one chunk (CPT == 1), so its
+                  // 16 fragments are read once and kept in registers
+};
+
+template <int S, typename IdT, int LMODE, int SEM, int XDT, int XMODE, bool SCALED>
+__global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
+                                                                       const uint16_t* __restrict__ x, int M,
+                                                                       int max_tiles) {
+  static_assert(!SCALED || LMODE == LM_A16, "scaled tables hold one 16-bit value per element");
+  constexpr bool XLDS = XMODE != XM_GLOBAL;
+  constexpr int PF = decode_prefetch<S, IdT>(), NV = sizeof(IdT);
   constexpr int ESZ = lds_entry_bytes<LMODE>();
+  constexpr int XR = 4;  // 16-byte x loads per thread kept in registers across the codebook staging
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int NW = blockDim.x >> 6;
   const int K = L.codebook_size;
   const int B = L.blocks_per_row;
   const int in = L.in_features;
+  const int M16 = M * 16;
   uint8_t* lds_cb = smem;
-  float* red = reinterpret_cast<float*>(smem + (size_t)S * K * ESZ);  // [2][NW][256]
-  uint16_t* xs = reinterpret_cast<uint16_t*>(red + 2 * NW * 256);    // [M][in] when XLDS
+  float* part = reinterpret_cast<float*>(smem + (size_t)S * K * ESZ);        // [max_tiles][NW][M * 16]
+  uint8_t* zrow = reinterpret_cast<uint8_t*>(part + (size_t)max_tiles * NW * M16);  // 256 zero bytes
+  uint16_t* xs = reinterpret_cast<uint16_t*>(zrow + 256);                    // [M][in] when XLDS
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -73,147 +144,247 @@ __global__ __launch_bounds__(kDecodeThreads) void rvq_decode_kernel(LayerArgs L,
   const int q = lane >> 4;
   const int nchunk = (B + 63) >> 6;
   const int CPT = (nchunk + NW - 1) / NW;
+  // tiles [t_begin, t_begin + n_tiles_wg): T split as evenly as possible
   const int T = L.n_tiles;
-  const int t_begin = (int)((int64_t)blockIdx.x * T / gridDim.x);
-  const int n_tiles_wg = (int)((int64_t)(blockIdx.x + 1) * T / gridDim.x) - t_begin;
+  const int tq = T / (int)gridDim.x, tr = T % (int)gridDim.x, bx = blockIdx.x;
+  const int t_begin = bx * tq + min(bx, tr);
+  const int n_tiles_wg = tq + (bx < tr ? 1 : 0);
   const int n_items = n_tiles_wg * CPT;
-  const uint32_t kmax = (uint32_t)(K - 1);
   const int xm = min(nl, M - 1);  // x row this lane feeds to the MFMA
+  // Index mask: ids are validated against K on the host; the mask keeps any
+  // other value inside the LDS allocation (next power of two of K entries).
+  const uint32_t kmask = K <= 1 ? 0u : (0xffffffffu >> __builtin_clz((uint32_t)(K - 1)));
 
-  if constexpr (XLDS) {
-    const int n16 = M * in / 8;  // in % 128 == 0
-    for (int i = tid; i < n16; i += kDecodeThreads)
-      reinterpret_cast<u32x4_t*>(xs)[i] = ldg128(x + (size_t)i * 8);
-    // the first codebook staging below ends with a barrier before any read
-  }
-
-  // ---- index prefetch ring (issue cursor runs PF items ahead) -------------
+  // ---- index ring: issue cursor runs PF items ahead of the compute cursor ----
   u32x4_t ring[PF][S][NV];
-  int is_t = 0, is_c = 0;  // issue cursor: tile offset within the range, chunk slot
-  FragTile<S> iti = get_frag_tile<S>(L, t_begin < T ? t_begin : 0);
-  auto issue = [&](u32x4_t (&dst)[S][NV]) {
+  uint32_t rsr[PF];  // raw bits of the lane's row scale for the slot's tile
+  int is_t = 0, is_c = 0;
+  FragTile<S> iti = tile_at<S>(L, t_begin);
+  auto issue = [&](int j) {
+    // Always issues the same buffer loads (straight-line code); a slot past
+    // the range, or a chunk past the row, gets an out-of-range offset and
+    // reads zeros without touching memory.  Rows past the tile re-read its
+    // last row (outputs of those rows are never stored).
     const int c = wave + NW * is_c;
-    const int base = c * 64 + 16 * q;
-    const bool ok = is_t < n_tiles_wg && c < nchunk && base < B && nl < iti.rows;
-    const int64_t r = iti.row0 + nl;
+    const bool ok = is_t < n_tiles_wg && c < nchunk;  // uniform
+    const int base = min(c * 64 + 16 * q, B - 16);
+    const int r = iti.row0 + min(nl, iti.rows - 1);
+    const uint32_t off = ok ? (uint32_t)((r * B + base) * (int)sizeof(IdT)) : kBufOOB;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const IdT* p = reinterpret_cast<const IdT*>(iti.p.ids[s]) + r * B + base;
+      const bufrsrc_t rs_ids = make_rsrc(iti.p.ids[s]);
 #pragma unroll
-      for (int v = 0; v < NV; ++v) dst[s][v] = ok ? ldg128_stream(p + v * (16 / NV)) : u32x4_t{0, 0, 0, 0};
+      for (int v = 0; v < NV; ++v) ring[j][s][v] = ldbuf128_stream(rs_ids, off + v * 16);
     }
+    // 16-bit scale buffers only (the host routes fp32 scales elsewhere)
+    const int si = (int)scale_index(L, SCALED ? iti.row0 : r);
+    rsr[j] = ldbuf16(make_rsrc(iti.p.row_scale), is_t < n_tiles_wg ? (uint32_t)si * 2u : kBufOOB);
     if (++is_c == CPT) {
       is_c = 0;
-      ++is_t;
-      if (is_t < n_tiles_wg) iti = get_frag_tile<S>(L, t_begin + is_t);
+      if (++is_t < n_tiles_wg) iti = tile_at<S>(L, t_begin + is_t);
     }
   };
 #pragma unroll
-  for (int j = 0; j < PF; ++j) issue(ring[j]);
+  for (int j = 0; j < PF; ++j) issue(j);
 
-  // ---- compute ------------------------------------------------------------
-  int staged = -1;
-  int buf = 0;
+  // ---- prologue: one memory round trip for activations and codebooks -------
+  // (issued after the ring, so the index loads are already in flight)
+  const int n16 = XLDS ? M * in / 8 : 0;  // 16-byte pieces of x (in % 128 == 0)
+  u32x4_t xr[XR];
+#pragma unroll
+  for (int u = 0; u < XR; ++u) xr[u] = ldg128(x + (size_t)min(tid + u * (int)blockDim.x, max(n16 - 1, 0)) * 8);
+  if (tid < 16) reinterpret_cast<u32x4_t*>(zrow)[tid] = u32x4_t{0, 0, 0, 0};
+  FragTile<S> cti = tile_at<S>(L, t_begin);
+  int staged = cti.group;
+  uint32_t staged_sc = 0;
+  {
+    // first codebook batch issued before the first tile's scale is read, so
+    // both round trips overlap
+    u32x4_t cbr[S][stage_batch<S>()];
+    if (D.cb_dtype != WAL_F32) load_codebook_batch<S>(cbr, cti.p, K, tid, blockDim.x);
+    const u32x4_t(*first)[S][stage_batch<S>()] = D.cb_dtype != WAL_F32 ? &cbr : nullptr;
+    if constexpr (SCALED) {
+      staged_sc = __builtin_amdgcn_readfirstlane(rsr[0]);  // the first tile's scale (ring slot 0)
+      stage_codebooks<S, LMODE, SEM, XDT, true>(
+          lds_cb, cti.p, K, D, make_row_scale<XDT>(scale_bits_to_f32(staged_sc, D.sc_dtype)), first);
+    } else {
+      stage_codebooks<S, LMODE, SEM, XDT, false>(lds_cb, cti.p, K, D, make_row_scale<XDT>(0.0f), first);
+    }
+  }
+  if constexpr (XLDS) {
+#pragma unroll
+    for (int u = 0; u < XR; ++u)
+      if (tid + u * (int)blockDim.x < n16) reinterpret_cast<u32x4_t*>(xs)[tid + u * blockDim.x] = xr[u];
+    for (int i = tid + XR * blockDim.x; i < n16; i += blockDim.x)
+      reinterpret_cast<u32x4_t*>(xs)[i] = ldg128(x + (size_t)i * 8);
+  }
+  __syncthreads();
+
+  // XM_REG: this wave's chunk is the same for every tile; read its 16 x
+  // fragments (zero past the row) once.
+  u32x4_t xreg[XMODE == XM_REG ? 16 : 1];
+  if constexpr (XMODE == XM_REG) {
+    const int base = wave * 64 + 16 * q;
+    const uint8_t* xp = base < B ? reinterpret_cast<const uint8_t*>(xs + (size_t)xm * in + (size_t)base * 8) : zrow;
+#pragma unroll
+    for (int tt = 0; tt < 16; ++tt) xreg[tt] = *reinterpret_cast<const u32x4_t*>(xp + tt * 16);
+  }
+
+  // ---- compute ----------------------------------------------------------------
   int ct_t = 0, ct_c = 0;  // compute cursor
-  FragTile<S> cti = iti;
   RowScale rs = make_row_scale<XDT>(0.0f);
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int i0 = 0; i0 < n_items; i0 += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      if (i0 + j >= n_items) break;  // uniform across the workgroup
-      if (ct_c == 0) {
-        cti = get_frag_tile<S>(L, t_begin + ct_t);
-        if (cti.group != staged) {
-          __syncthreads();  // every wave is done with the previous codebooks
-          stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, cti.p, K, D);
+      const bool live = i0 + j < n_items;  // uniform
+      if (live && ct_c == 0) {
+        // first item of a tile
+        cti = tile_at<S>(L, t_begin + ct_t);
+        bool restage = cti.group != staged;
+        uint32_t sc = 0;
+        if constexpr (SCALED) {
+          sc = __builtin_amdgcn_readfirstlane(rsr[j]);
+          restage = restage || sc != staged_sc;
+        }
+        if (restage) {
+          __syncthreads();  // every wave is done with the previous tables
+          if constexpr (SCALED) {
+            stage_codebooks<S, LMODE, SEM, XDT, true>(lds_cb, cti.p, K, D,
+                                                       make_row_scale<XDT>(scale_bits_to_f32(sc, D.sc_dtype)));
+          } else {
+            stage_codebooks<S, LMODE, SEM, XDT, false>(lds_cb, cti.p, K, D, make_row_scale<XDT>(0.0f));
+          }
           __syncthreads();
           staged = cti.group;
+          staged_sc = sc;
         }
-        const bool row_ok = nl < cti.rows;
-        const float rs_raw = row_ok ? load_f(cti.p.row_scale, D.sc_dtype, (cti.row0 + nl) / L.scale_rows) : 0.0f;
-        rs = make_row_scale<XDT>(rs_raw);
+        if constexpr (!SCALED) rs = make_row_scale<XDT>(scale_bits_to_f32(rsr[j], D.sc_dtype));
         acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       }
       const int c = wave + NW * ct_c;
-      const int base = c * 64 + 16 * q;
-      if (c < nchunk) {  // uniform across the wave
-        // activations: zero for blocks past the row (base >= B)
-        const bool seg_ok = base < B;
-        u32x4_t xf[16];
+      if (live && c < nchunk) {  // uniform across the wave
+        const int base = c * 64 + 16 * q;
+        const bool seg_ok = base < B;  // lanes past the row read zero activations
+        // lanes past the row read the 256-byte zero row instead
+        const uint8_t* xp = XLDS && seg_ok ? reinterpret_cast<const uint8_t*>(xs + (size_t)xm * in + (size_t)base * 8)
+                                           : zrow;
 #pragma unroll
         for (int tt = 0; tt < 16; ++tt) {
-          const int64_t off = (int64_t)xm * in + (int64_t)(base + tt) * 8;
-          if constexpr (XLDS) xf[tt] = seg_ok ? *reinterpret_cast<const u32x4_t*>(xs + off) : u32x4_t{0, 0, 0, 0};
-          else xf[tt] = seg_ok ? ldg128(x + off) : u32x4_t{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int tt = 0; tt < 16; ++tt) {
+          u32x4_t xf;
+          if constexpr (XMODE == XM_REG) {
+            xf = xreg[tt];
+          } else if constexpr (XMODE == XM_LDS) {
+            xf = *reinterpret_cast<const u32x4_t*>(xp + tt * 16);
+          } else {
+            xf = ldg128(x + (size_t)xm * in + (size_t)min(base + tt, B - 1) * 8);
+            if (!seg_ok) xf = u32x4_t{0, 0, 0, 0};
+          }
           uint32_t id[S];
 #pragma unroll
-          for (int s = 0; s < S; ++s) id[s] = min(extract_id<IdT>(ring[j][s], tt), kmax);
-          // rows past the tile hold a zero scale; their products are not stored
-          const u32x4_t w = make_wfrag<S, LMODE, SEM, XDT>(lds_cb, id, K, L.active_mask, rs);
-          acc = mfma16<XDT>(xf[tt], w, acc);
+          for (int s = 0; s < S; ++s) id[s] = extract_id<IdT>(ring[j][s], tt) & kmask;
+          u32x4_t w;
+          if constexpr (SCALED) w = *reinterpret_cast<const u32x4_t*>(lds_cb + (size_t)id[0] * 16);
+          else w = make_wfrag<S, LMODE, SEM, XDT>(lds_cb, id, K, L.active_mask, rs);
+          acc = mfma16<XDT>(xf, w, acc);
         }
       }
-      issue(ring[j]);  // refill this slot with the item PF ahead
-      if (++ct_c == CPT) {
-        // tile done: sum the NW partial accumulators, store M x 16 outputs
+      issue(j);  // refill this slot with the item PF ahead
+      if (live && ++ct_c == CPT) {
+        // tile done: park this wave's partial (rows m < M) in LDS
         ct_c = 0;
-        float* rb = red + (size_t)buf * NW * 256 + wave * 256;
+        float* pb = part + ((size_t)ct_t * NW + wave) * M16;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) rb[(4 * q + e) * 16 + nl] = acc[e];  // lane holds D[4q + e][nl]
-        __syncthreads();
-        if (tid < M * 16) {
-          const int m = tid >> 4;
-          const int n = tid & 15;
-          const float* rr = red + (size_t)buf * NW * 256 + tid;
-          float v = 0.0f;
-#pragma unroll
-          for (int w = 0; w < NW; ++w) v += rr[w * 256];
-          if (n < cti.rows) store_output(E, m, cti.out_row0 + n, v);
-        }
-        buf ^= 1;
+        for (int e = 0; e < 4; ++e)
+          if (4 * q + e < M) pb[(4 * q + e) * 16 + nl] = acc[e];  // lane holds D[4q + e][nl]
         ++ct_t;
       }
     }
   }
+
+  // ---- epilogue: sum the NW partials of every tile, store M x 16 outputs ----
+  // The only global stores of the kernel: none is pending while index loads
+  // are in flight, so the loads' waits stay in-order partial waits.
+  __syncthreads();
+  for (int e = tid; e < n_tiles_wg * M16; e += blockDim.x) {
+    const int k = e / M16;
+    const int o = e - k * M16;
+    const int m = o >> 4;
+    const int nn = o & 15;
+    const FragTile<S> ft = tile_at<S>(L, t_begin + k);
+    const float* pp = part + (size_t)k * NW * M16 + o;
+    float v = 0.0f;
+    for (int w = 0; w < NW; ++w) v += pp[w * M16];
+    if (nn < ft.rows) store_output(E, m, ft.out_row0 + nn, v);
+  }
 }
 
-template <int S, typename IdT, int LMODE, int SEM, int XDT>
+template <int S, typename IdT, int LMODE, int SEM, int XDT, bool SCALED>
 static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x, int M,
                             int n_cu, hipStream_t st) {
   constexpr int kLdsMax = 160 * 1024;
-  const bool xlds = decode_lds_bytes<LMODE>(S, L.codebook_size, true, M, L.in_features) <= (size_t)kLdsMax;
-  const size_t lds = decode_lds_bytes<LMODE>(S, L.codebook_size, xlds, M, L.in_features);
-  auto kern = xlds ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, true> : rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, false>;
-  static bool attr_set[2] = {false, false};
-  if (!attr_set[xlds]) {
+  const int nw = kDecodeMaxWaves;
+  const int S_ = S, K = L.codebook_size, in = L.in_features;
+  // Each workgroup takes an equal share of the tiles and keeps the partial
+  // sums of its whole share in LDS; when a share does not fit, the grid grows
+  // until it does.
+  auto plan_for = [&](int per_cu, bool xlds, int* grid, int* share) -> bool {
+    const size_t fixed = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, 0);
+    const size_t per_tile = (size_t)nw * M * 16 * sizeof(float);
+    const size_t avail = (size_t)kLdsMax / per_cu;
+    if (fixed + per_tile > avail) return false;
+    const int fit = (int)((avail - fixed) / per_tile);
+    int g = n_cu * per_cu < L.n_tiles ? n_cu * per_cu : L.n_tiles;
+    const int min_grid = (L.n_tiles + fit - 1) / fit;
+    if (g < min_grid) g = min_grid;
+    *grid = g;
+    *share = (L.n_tiles + g - 1) / g;
+    return true;
+  };
+  // One 8-wave workgroup per CU: measured faster than two co-resident ones
+  // (they contend for LDS gather bandwidth and stage the codebooks twice).
+  int grid = 0, share = 1;
+  bool xlds = true;
+  if (!plan_for(1, true, &grid, &share)) {
+    xlds = false;
+    if (!plan_for(1, false, &grid, &share)) return hipErrorInvalidValue;  // excluded by the host's eligibility check
+  }
+  const size_t lds = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, share);
+  if (grid < 1) return hipSuccess;
+  // one chunk per wave -> activation fragments stay in registers
+  const int nchunk = (L.blocks_per_row + 63) / 64;
+  const int xmode = !xlds ? XM_GLOBAL : (nchunk <= nw ? XM_REG : XM_LDS);
+  auto kern = xmode == XM_REG ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_REG, SCALED>
+              : xmode == XM_LDS ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_LDS, SCALED>
+                                : rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GLOBAL, SCALED>;
+  static bool attr_set[3] = {false, false, false};
+  if (!attr_set[xmode]) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                        kLdsMax);
     if (e != hipSuccess) return e;
-    attr_set[xlds] = true;
+    attr_set[xmode] = true;
   }
-  int per_cu = (int)(kLdsMax / lds);
-  if (per_cu > 4) per_cu = 4;
-  if (per_cu < 1) per_cu = 1;
-  int grid = n_cu * per_cu;
-  if (grid > L.n_tiles) grid = L.n_tiles;
-  if (grid < 1) return hipSuccess;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kDecodeThreads), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(nw * 64), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M,
+                     share);
   return hipGetLastError();
 }
 
 template <int S, typename IdT, int XDT>
 static hipError_t decode_sem(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
                              const void* x, int M, int n_cu, hipStream_t st) {
-  if (sem == SEM_FAST) return decode_go<S, IdT, LM_A16, SEM_FAST, XDT>(L, D, E, x, M, n_cu, st);
   if constexpr (S == 1) {
-    return decode_go<S, IdT, LM_A16, SEM_RECON, XDT>(L, D, E, x, M, n_cu, st);
+    // one stage: the row-scale product can be folded into the staged table
+    // when every 16-row tile has a single scale value
+    const bool scaled = L.scale_rows % 16 == 0;
+    if (sem == SEM_FAST)
+      return scaled ? decode_go<S, IdT, LM_A16, SEM_FAST, XDT, true>(L, D, E, x, M, n_cu, st)
+                    : decode_go<S, IdT, LM_A16, SEM_FAST, XDT, false>(L, D, E, x, M, n_cu, st);
+    return scaled ? decode_go<S, IdT, LM_A16, SEM_RECON, XDT, true>(L, D, E, x, M, n_cu, st)
+                  : decode_go<S, IdT, LM_A16, SEM_RECON, XDT, false>(L, D, E, x, M, n_cu, st);
   } else {
-    if (lmode == LM_H16) return decode_go<S, IdT, LM_H16, SEM_RECON, XDT>(L, D, E, x, M, n_cu, st);
-    return decode_go<S, IdT, LM_F32, SEM_RECON, XDT>(L, D, E, x, M, n_cu, st);
+    if (sem == SEM_FAST) return decode_go<S, IdT, LM_A16, SEM_FAST, XDT, false>(L, D, E, x, M, n_cu, st);
+    if (lmode == LM_H16) return decode_go<S, IdT, LM_H16, SEM_RECON, XDT, false>(L, D, E, x, M, n_cu, st);
+    return decode_go<S, IdT, LM_F32, SEM_RECON, XDT, false>(L, D, E, x, M, n_cu, st);
   }
 }
 

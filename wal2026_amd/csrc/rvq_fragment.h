@@ -78,123 +78,6 @@ WAL_DEVICE FragTile<S> get_frag_tile(const LayerArgs& L, int t) {
   return f;
 }
 
-// Convert one raw codebook entry (8 values; fp32 codebooks use both halves of
-// raw) of stage s into its LDS form at entry e.
-template <int LMODE, int SEM, int XDT>
-WAL_DEVICE void store_codebook_entry(uint8_t* lds, int e, int s, const u32x4_t (&raw)[2], int cb_dtype,
-                                            bool has_ss, float ss) {
-  if constexpr (LMODE == LM_H16) {
-    // fp16 copy.  Stage 0 is stored as 0 + v (-0 becomes +0), the first add
-    // of the reference's zero-initialised fp32 sum, so the fragment code can
-    // sum the stages without a leading zero.
-    u32x4_t a = raw[0];
-    if (s == 0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t w = a[j];
-        if ((w & 0xffffu) == 0x8000u) w &= 0xffff0000u;
-        if ((w >> 16) == 0x8000u) w &= 0x0000ffffu;
-        a[j] = w;
-      }
-    }
-    *reinterpret_cast<u32x4_t*>(lds + (size_t)e * 16) = a;
-  } else {
-    float v[8];
-    if (cb_dtype == WAL_F32) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) { v[j] = __uint_as_float(raw[0][j]); v[4 + j] = __uint_as_float(raw[1][j]); }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t w = raw[0][j];
-        if (cb_dtype == WAL_F16) { v[2 * j] = f16_to_f32(w & 0xffffu); v[2 * j + 1] = f16_to_f32(w >> 16); }
-        else { v[2 * j] = bf16_to_f32(w & 0xffffu); v[2 * j + 1] = bf16_to_f32(w >> 16); }
-      }
-    }
-    if constexpr (LMODE == LM_F32) {
-      // Stage 0 is stored as 0 + v (the reference's zero-initialised sum);
-      // -0 + u == u for every u, so other stages are stored unchanged.
-      const float z = s == 0 ? 0.0f : -0.0f;
-      u32x4_t a, b;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        a[j] = __float_as_uint(z + (has_ss ? v[j] * ss : v[j]));
-        b[j] = __float_as_uint(z + (has_ss ? v[4 + j] * ss : v[4 + j]));
-      }
-      u32x4_t* dst = reinterpret_cast<u32x4_t*>(lds + (size_t)e * 32);
-      dst[0] = a;
-      dst[1] = b;
-    } else {  // LM_A16
-      u32x4_t o;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t h[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const float x = v[2 * j + u];
-          float c;
-          if constexpr (SEM == SEM_FAST) {
-            c = round_dt<XDT>(x);
-            if (has_ss) c = round_dt<XDT>(c * round_dt<XDT>(ss));
-          } else {
-            c = 0.0f + (has_ss ? x * ss : x);
-          }
-          h[u] = to_bits16<XDT>(c);
-        }
-        o[j] = h[0] | (h[1] << 16);
-      }
-      *reinterpret_cast<u32x4_t*>(lds + (size_t)e * 16) = o;
-    }
-  }
-}
-
-// Fill LDS with the codebooks of one group (all threads of the block take
-// part).  16-bit codebooks: each thread issues the loads of 8 entries (over
-// the stages) before converting and storing any, so the load latency is paid
-// once per batch.  fp32 codebooks (rare) take a plain loop.
-template <int S, int LMODE, int SEM, int XDT>
-WAL_DEVICE void stage_codebooks(uint8_t* lds, const GroupPtrs<S>& g, int K, const DtypeArgs& D) {
-  constexpr int U = S >= 8 ? 1 : 8 / S;  // entries per stage per batch
-  const int nt = blockDim.x;
-  const bool has_ss = g.stage_scales != nullptr;
-  float ssv[S];
-#pragma unroll
-  for (int s = 0; s < S; ++s) ssv[s] = has_ss ? load_f(g.stage_scales, D.sc_dtype, s) : 1.0f;
-  if (D.cb_dtype == WAL_F32) {
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const char* cb = static_cast<const char*>(g.cb[s]);
-      for (int k = threadIdx.x; k < K; k += nt) {
-        const u32x4_t raw[2] = {ldg128(cb + (size_t)k * 32), ldg128(cb + (size_t)k * 32 + 16)};
-        store_codebook_entry<LMODE, SEM, XDT>(lds, s * K + k, s, raw, WAL_F32, has_ss, ssv[s]);
-      }
-    }
-    return;
-  }
-  for (int k0 = threadIdx.x; k0 < K; k0 += U * nt) {
-    u32x4_t raw[S][U];
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const char* cb = static_cast<const char*>(g.cb[s]);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int k = k0 + u * nt;
-        raw[s][u] = k < K ? ldg128(cb + (size_t)k * 16) : u32x4_t{0, 0, 0, 0};
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int k = k0 + u * nt;
-        if (k < K) {
-          const u32x4_t r2[2] = {raw[s][u], u32x4_t{0, 0, 0, 0}};
-          store_codebook_entry<LMODE, SEM, XDT>(lds, s * K + k, s, r2, D.cb_dtype, has_ss, ssv[s]);
-        }
-      }
-  }
-}
-
 // Row-scale operand: rf = rne_x(row_scale) as fp32.  For fp16 x, r2 is that
 // value as a packed fp16 pair; for bf16 x, r2 = (rf, 0) and r3 = (0, rf) as
 // packed bf16 pairs, the second operands of v_dot2_f32_bf16 below.
@@ -277,11 +160,170 @@ WAL_DEVICE u32x4_t scale_frag(const u32x4_t& a, const RowScale& rs) {
   }
 }
 
+// Round a pair to x dtype (nearest-even) and pack it: the hardware conversion,
+// exact for finite values.
 template <int XDT>
 WAL_DEVICE uint32_t pack_x(float lo, float hi) {
   if constexpr (XDT == WAL_F16) return pack_f16(lo, hi);
   else return pack_bf16(lo, hi);
 }
+
+// Convert one raw codebook entry (8 values; fp32 codebooks use both halves of
+// raw) of stage s into its LDS form at entry e.
+template <int LMODE, int SEM, int XDT, bool SCALE_TABLE>
+WAL_DEVICE void store_codebook_entry(uint8_t* lds, int e, int s, const u32x4_t (&raw)[2], int cb_dtype,
+                                     bool has_ss, float ss, const RowScale& rs) {
+  if constexpr (LMODE == LM_H16) {
+    // fp16 copy.  Stage 0 is stored as 0 + v (-0 becomes +0), the first add
+    // of the reference's zero-initialised fp32 sum, so the fragment code can
+    // sum the stages without a leading zero.
+    u32x4_t a = raw[0];
+    if (s == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t w = a[j];
+        if ((w & 0xffffu) == 0x8000u) w &= 0xffff0000u;
+        if ((w >> 16) == 0x8000u) w &= 0x0000ffffu;
+        a[j] = w;
+      }
+    }
+    *reinterpret_cast<u32x4_t*>(lds + (size_t)e * 16) = a;
+  } else if (LMODE == LM_A16 && SEM == SEM_RECON && cb_dtype == WAL_F16 && !has_ss) {
+    // The common case in one exact op per value: v_fma_mix_f32 converts the
+    // fp16 value and adds it to +0 (the reference's zero-initialised fp32
+    // sum), then a hardware nearest-even pack rounds the pair to x dtype.
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = pack_x<XDT>(mix_acc_lo(0.0f, raw[0][j]), mix_acc_hi(0.0f, raw[0][j]));
+    if constexpr (SCALE_TABLE) o = scale_frag<XDT>(o, rs);
+    *reinterpret_cast<u32x4_t*>(lds + (size_t)e * 16) = o;
+  } else {
+    float v[8];
+    if (cb_dtype == WAL_F32) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { v[j] = __uint_as_float(raw[0][j]); v[4 + j] = __uint_as_float(raw[1][j]); }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t w = raw[0][j];
+        if (cb_dtype == WAL_F16) { v[2 * j] = f16_to_f32(w & 0xffffu); v[2 * j + 1] = f16_to_f32(w >> 16); }
+        else { v[2 * j] = bf16_to_f32(w & 0xffffu); v[2 * j + 1] = bf16_to_f32(w >> 16); }
+      }
+    }
+    if constexpr (LMODE == LM_F32) {
+      // Stage 0 is stored as 0 + v (the reference's zero-initialised sum);
+      // -0 + u == u for every u, so other stages are stored unchanged.
+      const float z = s == 0 ? 0.0f : -0.0f;
+      u32x4_t a, b;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a[j] = __float_as_uint(z + (has_ss ? v[j] * ss : v[j]));
+        b[j] = __float_as_uint(z + (has_ss ? v[4 + j] * ss : v[4 + j]));
+      }
+      u32x4_t* dst = reinterpret_cast<u32x4_t*>(lds + (size_t)e * 32);
+      dst[0] = a;
+      dst[1] = b;
+    } else {  // LM_A16
+      // hardware round-to-nearest-even packs (finite codebooks)
+      u32x4_t o;
+      if constexpr (SEM == SEM_FAST) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = pack_x<XDT>(v[2 * j], v[2 * j + 1]);  // c = rne_x(cb)
+        if (has_ss) o = scale_frag<XDT>(o, make_row_scale<XDT>(ss));            // rne_x(c * rne_x(ss))
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a0 = has_ss ? v[2 * j] * ss : v[2 * j];
+          const float a1 = has_ss ? v[2 * j + 1] * ss : v[2 * j + 1];
+          o[j] = pack_x<XDT>(0.0f + a0, 0.0f + a1);  // rne_x(0 + v), the zero-initialised fp32 sum
+        }
+      }
+      if constexpr (SCALE_TABLE) o = scale_frag<XDT>(o, rs);
+      *reinterpret_cast<u32x4_t*>(lds + (size_t)e * 16) = o;
+    }
+  }
+}
+
+// Codebook staging.  16-bit codebooks go in batches: every thread issues the
+// loads of U entries per stage (entries k0 + u * nt) before converting and
+// storing any, so one batch costs one memory round trip; the loads are
+// straight-line (indices past K are clamped and their results dropped), so
+// callers can issue a batch early and store it later.
+template <int S>
+__host__ __device__ constexpr int stage_batch() { return S >= 8 ? 1 : 8 / S; }
+
+template <int S>
+WAL_DEVICE void load_codebook_batch(u32x4_t (&raw)[S][stage_batch<S>()], const GroupPtrs<S>& g, int K, int k0,
+                                    int nt) {
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const char* cb = static_cast<const char*>(g.cb[s]);
+#pragma unroll
+    for (int u = 0; u < stage_batch<S>(); ++u) raw[s][u] = ldg128(cb + (size_t)min(k0 + u * nt, K - 1) * 16);
+  }
+}
+
+// Stage scales of a group as fp32 (1.0 when absent).
+template <int S>
+WAL_DEVICE void load_stage_scales(float (&ssv)[S], const GroupPtrs<S>& g, const DtypeArgs& D) {
+#pragma unroll
+  for (int s = 0; s < S; ++s) ssv[s] = g.stage_scales != nullptr ? load_f(g.stage_scales, D.sc_dtype, s) : 1.0f;
+}
+
+template <int S, int LMODE, int SEM, int XDT, bool SCALE_TABLE>
+WAL_DEVICE void store_codebook_batch(uint8_t* lds, const u32x4_t (&raw)[S][stage_batch<S>()], int K, int k0, int nt,
+                                     const DtypeArgs& D, bool has_ss, const float (&ssv)[S], const RowScale& rs) {
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int u = 0; u < stage_batch<S>(); ++u) {
+      const int k = k0 + u * nt;
+      if (k < K) {
+        const u32x4_t r2[2] = {raw[s][u], u32x4_t{0, 0, 0, 0}};
+        store_codebook_entry<LMODE, SEM, XDT, SCALE_TABLE>(lds, s * K + k, s, r2, D.cb_dtype, has_ss, ssv[s], rs);
+      }
+    }
+}
+
+// Fill LDS with the codebooks of one group (all threads of the block take
+// part), 16-bit codebooks batch by batch; fp32 codebooks (rare) take a plain
+// loop.  SCALE_TABLE (LM_A16 only): every staged value is replaced by its
+// product with the row scale rs, rounded as the reference rounds
+// W = rne_x(a * rne_x(row_scale)).  first_batch_loaded: the caller already
+// issued the first batch into raw (load_codebook_batch with k0 = threadIdx.x).
+template <int S, int LMODE, int SEM, int XDT, bool SCALE_TABLE = false>
+WAL_DEVICE void stage_codebooks(uint8_t* lds, const GroupPtrs<S>& g, int K, const DtypeArgs& D,
+                                const RowScale& rs = RowScale{0.0f, 0u, 0u},
+                                const u32x4_t (*first)[S][stage_batch<S>()] = nullptr) {
+  static_assert(!SCALE_TABLE || LMODE == LM_A16, "scaled tables are 16-bit");
+  constexpr int U = stage_batch<S>();
+  const int nt = blockDim.x;
+  const bool has_ss = g.stage_scales != nullptr;
+  float ssv[S];
+  load_stage_scales<S>(ssv, g, D);
+  if (D.cb_dtype == WAL_F32) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const char* cb = static_cast<const char*>(g.cb[s]);
+      for (int k = threadIdx.x; k < K; k += nt) {
+        const u32x4_t raw[2] = {ldg128(cb + (size_t)k * 32), ldg128(cb + (size_t)k * 32 + 16)};
+        store_codebook_entry<LMODE, SEM, XDT, SCALE_TABLE>(lds, s * K + k, s, raw, WAL_F32, has_ss, ssv[s], rs);
+      }
+    }
+    return;
+  }
+  int k0 = threadIdx.x;
+  if (first != nullptr) {
+    store_codebook_batch<S, LMODE, SEM, XDT, SCALE_TABLE>(lds, *first, K, k0, nt, D, has_ss, ssv, rs);
+    k0 += U * nt;
+  }
+  for (; k0 < K; k0 += U * nt) {
+    u32x4_t raw[S][U];
+    load_codebook_batch<S>(raw, g, K, k0, nt);
+    store_codebook_batch<S, LMODE, SEM, XDT, SCALE_TABLE>(lds, raw, K, k0, nt, D, has_ss, ssv, rs);
+  }
+}
+
 
 // 8-weight fragment for stage ids id[0..S-1]: the pre-scale values in x
 // dtype (RECON: rne_x of the fp32 stage sum; FAST: the x-dtype stage sum),

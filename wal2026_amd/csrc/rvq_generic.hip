@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void rvq_dequant_kernel(LayerArgs L, DtypeArgs
     const int rr = (int)(slot / B);
     const int b = (int)(slot - (int64_t)rr * B);
     const int64_t r = ti.row0 + rr;
-    const float rs = load_f(g.row_scale, D.sc_dtype, r / L.scale_rows);
+    const float rs = load_f(g.row_scale, D.sc_dtype, scale_index(L, r));
     const int64_t orow = ti.out_row0 + rr;
     for (int j = 0; j < d; ++j) {
       const int col = b * d + j;
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void rvq_generic_linear_kernel(LayerArgs L, Dt
         const int64_t r = ti.row0 + rr;
         float rs = 1.0f;
         if (SEM != SEM_TRITON) {
-          const int64_t rsi = (SEM == SEM_ROUTE0 || SEM == SEM_ROUTE1) ? r : r / L.scale_rows;
+          const int64_t rsi = (SEM == SEM_ROUTE0 || SEM == SEM_ROUTE1) ? r : scale_index(L, r);
           rs = load_f(g.row_scale, D.sc_dtype, rsi);
         }
         w = weight_elem<SEM, DT>(L, g, D, r, col, rs);

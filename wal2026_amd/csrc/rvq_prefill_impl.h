@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void rvq_prefill_kernel(LayerArgs L, DtypeArgs
   const uint16_t* xrow = x + xm * in;
   const bool w_row_ok = lr < ti.rows;
   const int64_t wr = ti.row0 + lr;
-  const float rs_raw = w_row_ok ? load_f(ti.p.row_scale, D.sc_dtype, wr / L.scale_rows) : 0.0f;
+  const float rs_raw = w_row_ok ? load_f(ti.p.row_scale, D.sc_dtype, scale_index(L, wr)) : 0.0f;
   const RowScale rs = make_row_scale<XDT>(rs_raw);
   const IdT* idp[S];
 #pragma unroll

@@ -131,6 +131,11 @@ class _LayerDesc:
             for extra in (g.stage_scales, g.block_scale):
                 if extra is not None and extra.dtype != scale_dt:
                     raise NotImplementedError("wal2026_amd: scale buffers of one layer must share a dtype")
+        scale_rows, compact = _scale_runs(groups, row_slices)
+        if compact is not None:
+            for w, rs in zip(arr, compact):
+                w.row_scale = rs.data_ptr()
+        self.compact_scales = compact  # keeps the compact buffers alive
         L = _lib.WalLayer()
         L.in_features = in_features
         L.out_features = out_features
@@ -141,7 +146,7 @@ class _LayerDesc:
         L.id_dtype = _lib.id_tag(ids0.dtype)
         L.codebook_dtype = _lib.float_tag(cb0.dtype)
         L.scale_dtype = _lib.float_tag(scale_dt)
-        L.scale_rows = 1
+        L.scale_rows = scale_rows
         L.n_groups = len(groups)
         L.groups = ctypes.cast(arr, ctypes.POINTER(_lib.WalGroup))
         L.plan = None
@@ -158,6 +163,38 @@ class _LayerDesc:
             L.plan = self.plan.data_ptr()
         self.device = device
         self.key = _desc_key(groups)
+
+
+_SCALE_RUNS = (128, 64, 32, 16)
+
+
+def _scale_runs(groups, row_slices) -> tuple[int, list[Tensor] | None]:
+    """Longest R in _SCALE_RUNS such that every row group's row_scale is
+    constant (bit for bit) over aligned runs of R rows, with the compact
+    per-run copies of the groups' scales; (1, None) when there is none.
+
+    The reference keeps one scale per row (src/runtime.py:278); a layer whose
+    rows share scales in aligned runs (per-128-row-group scales expanded to
+    rows) gives the library the same values through a shorter buffer, and
+    with runs of 16 or more rows the decode kernel can fold the scale into its
+    staged codebook.  One host sync per candidate R, when the descriptor is
+    built."""
+    if groups[0].row_scale.dtype not in (torch.float16, torch.bfloat16):
+        return 1, None
+    bits = torch.cat([g.row_scale.reshape(-1).view(torch.int16) for g in groups])
+    for R in _SCALE_RUNS:
+        if any((r0 - row_slices[0][0]) % R for r0, _ in row_slices):
+            continue
+        comp = bits[::R]
+        if not torch.equal(comp.repeat_interleave(R)[: bits.numel()], bits):
+            continue
+        base = row_slices[0][0]
+        compact = []
+        for (r0, r1), g in zip(row_slices, groups):
+            lo, hi = (r0 - base) // R, -(-(r1 - base) // R)
+            compact.append(comp[lo:hi].view(g.row_scale.dtype).contiguous())
+        return R, compact
+    return 1, None
 
 
 def _desc_key(groups) -> tuple:
