@@ -30,7 +30,7 @@ extern "C" {
 #endif
 
 #define WAL_RVQ_MAX_STAGES 8
-#define WAL_ABI_VERSION 1
+#define WAL_ABI_VERSION 2
 
 typedef enum wal_dtype {
   WAL_U8 = 0,   /* index planes, codebook_size <= 256 (src/block_vq.py:160-165) */
@@ -89,10 +89,11 @@ typedef struct wal_rvq_layer {
   int32_t scale_dtype;      /* row_scale, stage_scales and block_scale dtype */
   int32_t scale_rows;       /* rows per row_scale entry; 1 = per row */
   int32_t n_groups;
-  int32_t reserved;
+  int32_t image_tag;        /* WAL_RVQ_IMAGE_TAG the image was built for; 0 = no image */
   const wal_rvq_group* groups;  /* host array [n_groups]; groups[g].row0 ascending, contiguous */
   const void* plan;             /* device copy of the plan (see wal_rvq_plan_build),
                                    required when n_groups > 1, else may be NULL */
+  const void* image;            /* device codebook image (wal_rvq_image_build) or NULL */
 } wal_rvq_layer;
 
 /* ---- plan: device-side group and tile tables ---------------------------- */
@@ -107,6 +108,30 @@ int wal_rvq_plan_size(const wal_rvq_layer* layer, size_t* bytes);
  * device pointer in layer->plan.  The image embeds the group device pointers,
  * so it must be rebuilt if any buffer moves. */
 int wal_rvq_plan_build(const wal_rvq_layer* layer, void* dst, size_t bytes);
+
+/* ---- codebook images ------------------------------------------------------ */
+
+/* Tag of an image built for calls with this semantics and activation dtype. */
+#define WAL_RVQ_IMAGE_TAG(semantics, x_dtype) (0x1000 | ((semantics) & 0xf) | (((x_dtype) & 0xff) << 4))
+
+/* Bytes of the codebook image of this layer for calls with the given
+ * semantics (wal_rvq_semantics) and activation dtype.  No reference
+ * counterpart as an entry point: it is the device-side form of the derived
+ * codebook caches the reference keeps on its modules (the out_dtype copies of
+ * _build_fast_cache, src/runtime.py:431-448; the stage-scale-folded stack of
+ * _triton_state, src/runtime.py:855-876). */
+int wal_rvq_image_size(const wal_rvq_layer* layer, int semantics, int x_dtype, size_t* bytes);
+
+/* Convert every group's codebooks, once, into the form the fused kernels
+ * stage in LDS (per-stage values already rounded as the reference's
+ * dequantisation rounds them before the row scale) and write it to device
+ * memory dst (16-byte aligned, `bytes` from wal_rvq_image_size).  To use it,
+ * store dst in layer->image and WAL_RVQ_IMAGE_TAG(semantics, x_dtype) in
+ * layer->image_tag; wal_rvq_linear refuses a call whose semantics or x dtype
+ * differ from the tag.  Rebuild it when a codebook or stage scale changes.
+ * Finite codebooks and scales (the fused kernels' contract). */
+int wal_rvq_image_build(const wal_rvq_layer* layer, int semantics, int x_dtype, void* dst, size_t bytes,
+                        void* stream);
 
 /* ---- Block-RVQ entry points --------------------------------------------- */
 

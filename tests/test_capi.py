@@ -146,3 +146,38 @@ def test_id_route_argument_checks():
     rc = lib.wal_id_route_linear(0x1000, 1, 64, _lib.BF16, 0x2000, _lib.I16, 8, 0x3000, 100, _lib.F16, 0x4000,
                                  None, _lib.F32, 2, 0x5000, _lib.BF16, None)
     assert rc == _lib.EINVAL and "mode" in lib.wal_last_error().decode()
+
+
+def test_image_size_and_argument_checks():
+    """Codebook image bytes: per group S x K entries of 16 bytes (32 for the
+    fp32 form used by multi-stage layers with stage scales or non-fp16
+    codebooks); unsupported layouts and dtypes are refused on the host."""
+    lib = _lib.lib()
+    size = ctypes.c_size_t(0)
+    L, _g = _fake_layer([64, 64], S=2, K=256, plan=0x5000)
+    assert lib.wal_rvq_image_size(ctypes.byref(L), _lib.RECONSTRUCT, _lib.BF16, ctypes.byref(size)) == _lib.OK
+    assert size.value == 2 * 2 * 256 * 16
+    L.codebook_dtype = _lib.BF16  # multi-stage sums of bf16 codebooks are staged as fp32 values
+    assert lib.wal_rvq_image_size(ctypes.byref(L), _lib.RECONSTRUCT, _lib.BF16, ctypes.byref(size)) == _lib.OK
+    assert size.value == 2 * 2 * 256 * 32
+    assert lib.wal_rvq_image_size(ctypes.byref(L), _lib.RECONSTRUCT_FAST, _lib.F16, ctypes.byref(size)) == _lib.OK
+    assert size.value == 2 * 2 * 256 * 16
+    assert lib.wal_rvq_image_size(ctypes.byref(L), _lib.RECONSTRUCT, _lib.F32, ctypes.byref(size)) == _lib.EINVAL
+    L4, _g4 = _fake_layer([64], block=4)
+    assert lib.wal_rvq_image_size(ctypes.byref(L4), _lib.RECONSTRUCT, _lib.BF16,
+                                  ctypes.byref(size)) == _lib.EUNSUPPORTED
+    # dst must be aligned and large enough (refused before any launch)
+    L1, _g1 = _fake_layer([64], S=1, K=256)
+    assert lib.wal_rvq_image_build(ctypes.byref(L1), 0, _lib.BF16, 0x1008, 1 << 20, None) == _lib.EINVAL
+    assert lib.wal_rvq_image_build(ctypes.byref(L1), 0, _lib.BF16, 0x1000, 16, None) == _lib.ESIZE
+
+
+def test_linear_refuses_mismatched_image():
+    """An image built for another semantics or activation dtype is refused."""
+    L, _g = _fake_layer([64], S=1, K=256)
+    L.image = 0x7000
+    L.image_tag = _lib.image_tag(_lib.RECONSTRUCT, _lib.F16)
+    lib = _lib.lib()
+    rc = lib.wal_rvq_linear(ctypes.byref(L), _lib.RECONSTRUCT, 0, 0x1000, 1, _lib.BF16, None, _lib.F32, 0x2000,
+                            _lib.BF16, None)
+    assert rc == _lib.EINVAL and "image" in lib.wal_last_error().decode()

@@ -14,7 +14,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libwal2026_amd.so"
 
 MAX_STAGES = 8
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # wal_dtype
 U8, I16, U16, I32 = 0, 1, 2, 3
@@ -33,6 +33,8 @@ ID_DTYPES = {torch.uint8: U8, torch.int16: I16, torch.uint16: U16, torch.int32: 
 EXPORTED_SYMBOLS = (
     "wal_rvq_plan_size",
     "wal_rvq_plan_build",
+    "wal_rvq_image_size",
+    "wal_rvq_image_build",
     "wal_rvq_reconstruct",
     "wal_rvq_linear",
     "wal_rvq_group_linear_matmul",
@@ -72,10 +74,16 @@ class WalLayer(ctypes.Structure):
         ("scale_dtype", ctypes.c_int32),
         ("scale_rows", ctypes.c_int32),
         ("n_groups", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("image_tag", ctypes.c_int32),
         ("groups", ctypes.POINTER(WalGroup)),
         ("plan", ctypes.c_void_p),
+        ("image", ctypes.c_void_p),
     ]
+
+
+def image_tag(semantics: int, x_dtype_tag: int) -> int:
+    """WAL_RVQ_IMAGE_TAG(semantics, x_dtype)."""
+    return 0x1000 | (semantics & 0xF) | ((x_dtype_tag & 0xFF) << 4)
 
 
 class WalError(RuntimeError):
@@ -100,6 +108,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wal_rvq_plan_size.argtypes = [ctypes.POINTER(WalLayer), ctypes.POINTER(sz)]
     L.wal_rvq_plan_build.restype = i32
     L.wal_rvq_plan_build.argtypes = [ctypes.POINTER(WalLayer), vp, sz]
+    L.wal_rvq_image_size.restype = i32
+    L.wal_rvq_image_size.argtypes = [ctypes.POINTER(WalLayer), i32, i32, ctypes.POINTER(sz)]
+    L.wal_rvq_image_build.restype = i32
+    L.wal_rvq_image_build.argtypes = [ctypes.POINTER(WalLayer), i32, i32, vp, sz, vp]
     L.wal_rvq_reconstruct.restype = i32
     L.wal_rvq_reconstruct.argtypes = [ctypes.POINTER(WalLayer), i32, u32, vp, i32, vp]
     L.wal_rvq_linear.restype = i32

@@ -132,6 +132,8 @@ LayerArgs make_args(const wal_rvq_layer& L, int kind, uint32_t active_mask) {
   A.active_mask = active_mask;
   A.plan = L.n_groups > 1 ? reinterpret_cast<const PlanHeader*>(L.plan) : nullptr;
   A.g0 = L.groups[0];
+  A.n_groups = L.n_groups;
+  A.image = nullptr;
   return A;
 }
 
@@ -249,6 +251,49 @@ int wal_rvq_plan_build(const wal_rvq_layer* layer, void* dst, size_t bytes) {
   return WAL_OK;
 }
 
+// Image bytes: per group, S x K entries of the LdsMode entry size.
+size_t image_bytes(const wal_rvq_layer& L, int sem) {
+  const int esz = lds_mode_for(L, sem) == LM_F32 ? 32 : 16;
+  return (size_t)L.n_groups * L.num_stages * L.codebook_size * esz;
+}
+
+int image_args(const wal_rvq_layer* layer, int semantics, int x_dtype, int* sem) {
+  int rc = validate_layer(layer);
+  if (rc) return rc;
+  if (layer->block_size != 8) return fail(WAL_EUNSUPPORTED, "codebook images are for block_size 8 (got %d)", layer->block_size);
+  if (layer->num_stages > 4) return fail(WAL_EUNSUPPORTED, "codebook images are for at most 4 stages");
+  if (!is_half_dtype(x_dtype)) return fail(WAL_EINVAL, "x dtype must be F16 or BF16 (got %d)", x_dtype);
+  return resolve_semantics(*layer, semantics, sem);
+}
+
+int wal_rvq_image_size(const wal_rvq_layer* layer, int semantics, int x_dtype, size_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return fail(WAL_EINVAL, "bytes is NULL");
+  int sem = 0;
+  int rc = image_args(layer, semantics, x_dtype, &sem);
+  if (rc) return rc;
+  *bytes = image_bytes(*layer, sem);
+  return WAL_OK;
+}
+
+int wal_rvq_image_build(const wal_rvq_layer* layer, int semantics, int x_dtype, void* dst, size_t bytes,
+                        void* stream) {
+  g_err[0] = 0;
+  int sem = 0;
+  int rc = image_args(layer, semantics, x_dtype, &sem);
+  if (rc) return rc;
+  if (!dst || !aligned16(dst)) return fail(WAL_EINVAL, "dst must be a 16-byte aligned device pointer");
+  const size_t need = image_bytes(*layer, sem);
+  if (bytes < need) return fail(WAL_ESIZE, "image needs %zu bytes, got %zu", need, bytes);
+  for (int g = 0; g < layer->n_groups; ++g)
+    for (int s = 0; s < layer->num_stages; ++s)
+      if (!aligned16(layer->groups[g].codebooks[s])) return fail(WAL_EINVAL, "codebooks must be 16-byte aligned");
+  LayerArgs A = make_args(*layer, 0, resolve_mask(*layer, 0));
+  DtypeArgs D{layer->id_dtype, layer->codebook_dtype, layer->scale_dtype, x_dtype};
+  hipError_t e = launch_image(A, D, sem, lds_mode_for(*layer, sem), dst, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_image_build launch");
+}
+
 int wal_rvq_reconstruct(const wal_rvq_layer* layer, int semantics, uint32_t active_stage_mask, void* w_out,
                         int out_dtype, void* stream) {
   g_err[0] = 0;
@@ -282,8 +327,12 @@ int wal_rvq_linear(const wal_rvq_layer* layer, int semantics, uint32_t active_st
   DtypeArgs D{layer->id_dtype, layer->codebook_dtype, layer->scale_dtype, x_dtype};
   EpilogueArgs E{y, bias, (int64_t)layer->out_features, y_dtype, x_dtype, bias_dtype, bias ? 1 : 0};
   hipError_t e;
+  if (layer->image != nullptr && layer->image_tag != WAL_RVQ_IMAGE_TAG(semantics, x_dtype))
+    return fail(WAL_EINVAL, "the layer's codebook image was built for tag 0x%x, this call needs 0x%x",
+                layer->image_tag, WAL_RVQ_IMAGE_TAG(semantics, x_dtype));
   if (m <= 16 && mfma_eligible(*layer, sem, x_dtype, x, false)) {
     LayerArgs A = make_args(*layer, 0, mask);
+    A.image = static_cast<const uint8_t*>(layer->image);
     e = launch_decode(A, D, E, sem, lds_mode_for(*layer, sem), x, (int)m, device_cu_count(), st);
   } else if (m > 16 && mfma_eligible(*layer, sem, x_dtype, x, true)) {
     LayerArgs A = make_args(*layer, 2, mask);

@@ -103,6 +103,9 @@ struct LayerArgs {
   int32_t scale_shift;   // log2(scale_rows) when it is a power of two, else -1
   const PlanHeader* plan;  // NULL -> single group g0
   wal_rvq_group g0;
+  const uint8_t* image;    // codebook image (per group: S x K staged entries) or NULL
+  int32_t n_groups;
+  int32_t pad2;
 };
 
 // row_scale entry of row r (inside its group): r / scale_rows, a shift when

@@ -58,12 +58,13 @@ WAL_DEVICE uint32_t extract_id(const u32x4_t (&v)[sizeof(IdT)], int t) {
   }
 }
 
-// Bytes of LDS a decode launch needs: codebooks, the per-tile partial sums of
-// every wave (max_tiles tiles per workgroup), a 256-byte zero row and (xlds)
-// the activation rows.
+// Bytes of LDS a decode launch needs: nslots staged tables (the codebooks of
+// up to two groups / scale runs), the per-tile partial sums of every wave
+// (max_tiles tiles per workgroup), a 256-byte zero row and (xlds) the
+// activation rows.
 template <int LMODE>
-WAL_HOST_DEVICE size_t decode_lds_bytes(int S, int K, bool xlds, int M, int in, int nw, int max_tiles) {
-  return (size_t)S * K * lds_entry_bytes<LMODE>() + (size_t)max_tiles * nw * M * 16 * sizeof(float) + 256 +
+WAL_HOST_DEVICE size_t decode_lds_bytes(int S, int K, bool xlds, int M, int in, int nw, int max_tiles, int nslots) {
+  return (size_t)nslots * S * K * lds_entry_bytes<LMODE>() + (size_t)max_tiles * nw * M * 16 * sizeof(float) + 256 +
          (xlds ? (size_t)M * in * sizeof(uint16_t) : 0);
 }
 
@@ -84,6 +85,7 @@ WAL_DEVICE FragTile<S> tile_at(const LayerArgs& L, int t) {
     f.row0 = t * 16;
     f.rows = min(16, L.g0.rows - f.row0);
     f.out_row0 = L.g0.row0 + f.row0;
+    f.grows = L.g0.rows;
   } else {
     typedef const __attribute__((address_space(4))) PlanHeader c_header_t;
     typedef const __attribute__((address_space(4))) PlanTile c_tile_t;
@@ -103,11 +105,36 @@ WAL_DEVICE FragTile<S> tile_at(const LayerArgs& L, int t) {
     f.row0 = pt->row0;
     f.rows = pt->rows;
     f.out_row0 = pt->out_row0;
+    f.grows = G->rows;
   }
   return f;
 }
 
+// Staged-table key of a tile: its group, and for scaled tables its scale run.
+template <int S, bool SCALED>
+WAL_DEVICE int table_key(const LayerArgs& L, const FragTile<S>& f) {
+  return SCALED ? (f.group << 16) ^ (int)scale_index(L, f.row0) : f.group;
+}
+
 WAL_DEVICE float scale_bits_to_f32(uint32_t h, int dt) { return dt == WAL_F16 ? f16_to_f32(h) : bf16_to_f32(h); }
+
+// Stage one table (a group's codebooks, scaled by rs for SCALE_TABLE) from
+// the image when there is one, else from the raw codebooks.  Out of line: the
+// rare paths that call it (restaging in the loop, a launch without an image)
+// then cost one copy of this code instead of one per unrolled pipeline slot;
+// the kernels are small enough to stay in the instruction cache.
+//
+// The destination is an offset into the dynamic LDS (decode_smem), so the
+// stores stay LDS stores inside the out-of-line function.
+extern __shared__ __attribute__((aligned(16))) uint8_t decode_smem[];
+
+template <int S, int LMODE, int SEM, int XDT, bool SCALE_TABLE>
+__device__ __attribute__((noinline)) void stage_table(uint32_t dst_off, const uint8_t* img, GroupPtrs<S> p, int K,
+                                                      DtypeArgs D, RowScale rs) {
+  uint8_t* dst = decode_smem + dst_off;
+  if (img != nullptr) stage_image<XDT, SCALE_TABLE>(dst, img, S * K * lds_entry_bytes<LMODE>() / 16, rs);
+  else stage_codebooks<S, LMODE, SEM, XDT, SCALE_TABLE>(dst, p, K, D, rs);
+}
 
 // Where the MFMA's activation fragments come from.
 enum XMode : int {
@@ -120,20 +147,21 @@ enum XMode : int {
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int XMODE, bool SCALED>
 __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
                                                                        const uint16_t* __restrict__ x, int M,
-                                                                       int max_tiles) {
+                                                                       int max_tiles, int nslots) {
   static_assert(!SCALED || LMODE == LM_A16, "scaled tables hold one 16-bit value per element");
   constexpr bool XLDS = XMODE != XM_GLOBAL;
   constexpr int PF = decode_prefetch<S, IdT>(), NV = sizeof(IdT);
   constexpr int ESZ = lds_entry_bytes<LMODE>();
   constexpr int XR = 4;  // 16-byte x loads per thread kept in registers across the codebook staging
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int NW = blockDim.x >> 6;
+  uint8_t* smem = decode_smem;
+  constexpr int NW = kDecodeMaxWaves;  // launched with exactly NW waves
   const int K = L.codebook_size;
   const int B = L.blocks_per_row;
   const int in = L.in_features;
   const int M16 = M * 16;
-  uint8_t* lds_cb = smem;
-  float* part = reinterpret_cast<float*>(smem + (size_t)S * K * ESZ);        // [max_tiles][NW][M * 16]
+  const int tbl_bytes = S * K * ESZ;  // one staged table (all stages of a group)
+  uint8_t* lds_cb = smem;             // nslots (1 or 2) table slots
+  float* part = reinterpret_cast<float*>(smem + (size_t)nslots * tbl_bytes);  // [max_tiles][NW][M * 16]
   uint8_t* zrow = reinterpret_cast<uint8_t*>(part + (size_t)max_tiles * NW * M16);  // 256 zero bytes
   uint16_t* xs = reinterpret_cast<uint16_t*>(zrow + 256);                    // [M][in] when XLDS
 
@@ -149,6 +177,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   const int tq = T / (int)gridDim.x, tr = T % (int)gridDim.x, bx = blockIdx.x;
   const int t_begin = bx * tq + min(bx, tr);
   const int n_tiles_wg = tq + (bx < tr ? 1 : 0);
+  const int t_end = t_begin + n_tiles_wg;
   const int n_items = n_tiles_wg * CPT;
   const int xm = min(nl, M - 1);  // x row this lane feeds to the MFMA
   // Index mask: ids are validated against K on the host; the mask keeps any
@@ -187,29 +216,54 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
 #pragma unroll
   for (int j = 0; j < PF; ++j) issue(j);
 
-  // ---- prologue: one memory round trip for activations and codebooks -------
-  // (issued after the ring, so the index loads are already in flight)
+  // ---- prologue: one memory round trip for activations and tables -----------
+  // The range's tiles fall in one or two table segments (same group and, for
+  // scaled tables, same scale run): the segment boundary is where the first
+  // tile's group or scale run ends.  Both segments' tables are staged now,
+  // into slots 0 and 1; a third segment (rare: a range longer than a group)
+  // is restaged in the loop.
+  FragTile<S> cti = tile_at<S>(L, t_begin);
+  int seg1 = t_begin + (cti.grows - cti.row0 + 15) / 16;  // first tile of the next group
+  if constexpr (SCALED) {
+    const int run_left = L.scale_rows - (cti.row0 & (L.scale_rows - 1));  // scale_rows: power of two >= 16
+    seg1 = min(seg1, t_begin + run_left / 16);
+  }
+  const bool two = seg1 < t_end && nslots == 2;
+  FragTile<S> sti = two ? tile_at<S>(L, seg1) : cti;
+  int key[2] = {table_key<S, SCALED>(L, cti), two ? table_key<S, SCALED>(L, sti) : -1};
+  const uint8_t* img0 = L.image != nullptr ? L.image + (size_t)cti.group * tbl_bytes : nullptr;
+  const uint8_t* img1 = L.image != nullptr ? L.image + (size_t)sti.group * tbl_bytes : nullptr;
   const int n16 = XLDS ? M * in / 8 : 0;  // 16-byte pieces of x (in % 128 == 0)
   u32x4_t xr[XR];
 #pragma unroll
   for (int u = 0; u < XR; ++u) xr[u] = ldg128(x + (size_t)min(tid + u * (int)blockDim.x, max(n16 - 1, 0)) * 8);
   if (tid < 16) reinterpret_cast<u32x4_t*>(zrow)[tid] = u32x4_t{0, 0, 0, 0};
-  FragTile<S> cti = tile_at<S>(L, t_begin);
-  int staged = cti.group;
-  uint32_t staged_sc = 0;
-  {
-    // first codebook batch issued before the first tile's scale is read, so
-    // both round trips overlap
-    u32x4_t cbr[S][stage_batch<S>()];
-    if (D.cb_dtype != WAL_F32) load_codebook_batch<S>(cbr, cti.p, K, tid, blockDim.x);
-    const u32x4_t(*first)[S][stage_batch<S>()] = D.cb_dtype != WAL_F32 ? &cbr : nullptr;
+  uint32_t sc1 = 0;
+  if (L.image != nullptr) {
+    // first batches of both tables issued before the scales are read, so all
+    // the prologue's loads share one round trip
+    const int t16 = tbl_bytes / 16;
+    u32x4_t b0[kImageBatch], b1[kImageBatch];
+    load_image_batch(b0, img0, t16, tid, blockDim.x);
+    if (two) load_image_batch(b1, img1, t16, tid, blockDim.x);
+    if constexpr (SCALED) sc1 = two ? (uint32_t)ldg<uint16_t>(sti.p.row_scale, scale_index(L, sti.row0)) : 0u;
+    RowScale r0 = make_row_scale<XDT>(0.0f), r1 = r0;
     if constexpr (SCALED) {
-      staged_sc = __builtin_amdgcn_readfirstlane(rsr[0]);  // the first tile's scale (ring slot 0)
-      stage_codebooks<S, LMODE, SEM, XDT, true>(
-          lds_cb, cti.p, K, D, make_row_scale<XDT>(scale_bits_to_f32(staged_sc, D.sc_dtype)), first);
-    } else {
-      stage_codebooks<S, LMODE, SEM, XDT, false>(lds_cb, cti.p, K, D, make_row_scale<XDT>(0.0f), first);
+      r0 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(rsr[0]), D.sc_dtype));
+      r1 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(sc1), D.sc_dtype));
     }
+    stage_image<XDT, SCALED>(lds_cb, img0, t16, r0, &b0);
+    if (two) stage_image<XDT, SCALED>(lds_cb + tbl_bytes, img1, t16, r1, &b1);
+  } else {
+    // no image: convert the raw codebooks here (out of line)
+    RowScale r0 = make_row_scale<XDT>(0.0f), r1 = r0;
+    if constexpr (SCALED) {
+      sc1 = two ? (uint32_t)ldg<uint16_t>(sti.p.row_scale, scale_index(L, sti.row0)) : 0u;
+      r0 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(rsr[0]), D.sc_dtype));
+      r1 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(sc1), D.sc_dtype));
+    }
+    stage_table<S, LMODE, SEM, XDT, SCALED>(0u, nullptr, cti.p, K, D, r0);
+    if (two) stage_table<S, LMODE, SEM, XDT, SCALED>((uint32_t)tbl_bytes, nullptr, sti.p, K, D, r1);
   }
   if constexpr (XLDS) {
 #pragma unroll
@@ -228,10 +282,16 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
     const uint8_t* xp = base < B ? reinterpret_cast<const uint8_t*>(xs + (size_t)xm * in + (size_t)base * 8) : zrow;
 #pragma unroll
     for (int tt = 0; tt < 16; ++tt) xreg[tt] = *reinterpret_cast<const u32x4_t*>(xp + tt * 16);
+    // Opaque to the compiler, so it keeps them in registers instead of
+    // re-reading LDS next to each MFMA (waiting on the newest LDS read is a
+    // full lgkmcnt(0) wait, which would serialise the gathers).
+#pragma unroll
+    for (int tt = 0; tt < 16; ++tt) asm volatile("" : "+v"(xreg[tt]));
   }
 
   // ---- compute ----------------------------------------------------------------
   int ct_t = 0, ct_c = 0;  // compute cursor
+  int slot = 0;            // table slot of the current tile
   RowScale rs = make_row_scale<XDT>(0.0f);
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int i0 = 0; i0 < n_items; i0 += PF) {
@@ -239,25 +299,25 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
     for (int j = 0; j < PF; ++j) {
       const bool live = i0 + j < n_items;  // uniform
       if (live && ct_c == 0) {
-        // first item of a tile
+        // first item of a tile: pick its table slot
         cti = tile_at<S>(L, t_begin + ct_t);
-        bool restage = cti.group != staged;
-        uint32_t sc = 0;
-        if constexpr (SCALED) {
-          sc = __builtin_amdgcn_readfirstlane(rsr[j]);
-          restage = restage || sc != staged_sc;
-        }
-        if (restage) {
-          __syncthreads();  // every wave is done with the previous tables
-          if constexpr (SCALED) {
-            stage_codebooks<S, LMODE, SEM, XDT, true>(lds_cb, cti.p, K, D,
-                                                       make_row_scale<XDT>(scale_bits_to_f32(sc, D.sc_dtype)));
-          } else {
-            stage_codebooks<S, LMODE, SEM, XDT, false>(lds_cb, cti.p, K, D, make_row_scale<XDT>(0.0f));
-          }
+        const int k = table_key<S, SCALED>(L, cti);
+        if (k == key[0]) {
+          slot = 0;
+        } else if (k == key[1]) {
+          slot = 1;
+        } else {
+          // a segment no slot holds: restage into the slot the previous tile
+          // did not use (the only slot when there is one)
+          slot = nslots == 2 ? slot ^ 1 : 0;
+          __syncthreads();  // every wave is done with that slot
+          RowScale r = make_row_scale<XDT>(0.0f);
+          if constexpr (SCALED) r = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(rsr[j]), D.sc_dtype));
+          stage_table<S, LMODE, SEM, XDT, SCALED>((uint32_t)(slot * tbl_bytes),
+                                                  L.image != nullptr ? L.image + (size_t)cti.group * tbl_bytes : nullptr,
+                                                  cti.p, K, D, r);
           __syncthreads();
-          staged = cti.group;
-          staged_sc = sc;
+          key[slot] = k;
         }
         if constexpr (!SCALED) rs = make_row_scale<XDT>(scale_bits_to_f32(rsr[j], D.sc_dtype));
         acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -269,6 +329,21 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
         // lanes past the row read the 256-byte zero row instead
         const uint8_t* xp = XLDS && seg_ok ? reinterpret_cast<const uint8_t*>(xs + (size_t)xm * in + (size_t)base * 8)
                                            : zrow;
+        const uint8_t* tbl = lds_cb + (size_t)slot * tbl_bytes;
+        // All 16 fragments of the item are gathered before the first MFMA
+        // consumes one, so the LDS latency is paid once per item instead of
+        // once per block.
+        u32x4_t wf[16];
+#pragma unroll
+        for (int tt = 0; tt < 16; ++tt) {
+          uint32_t id[S];
+#pragma unroll
+          for (int s = 0; s < S; ++s) id[s] = extract_id<IdT>(ring[j][s], tt) & kmask;
+          if constexpr (SCALED) wf[tt] = *reinterpret_cast<const u32x4_t*>(tbl + (size_t)id[0] * 16);
+          else wf[tt] = make_wfrag<S, LMODE, SEM, XDT>(tbl, id, K, L.active_mask, rs);
+        }
+        // keep the scheduler from sinking the gathers back next to their MFMAs
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int tt = 0; tt < 16; ++tt) {
           u32x4_t xf;
@@ -280,16 +355,10 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
             xf = ldg128(x + (size_t)xm * in + (size_t)min(base + tt, B - 1) * 8);
             if (!seg_ok) xf = u32x4_t{0, 0, 0, 0};
           }
-          uint32_t id[S];
-#pragma unroll
-          for (int s = 0; s < S; ++s) id[s] = extract_id<IdT>(ring[j][s], tt) & kmask;
-          u32x4_t w;
-          if constexpr (SCALED) w = *reinterpret_cast<const u32x4_t*>(lds_cb + (size_t)id[0] * 16);
-          else w = make_wfrag<S, LMODE, SEM, XDT>(lds_cb, id, K, L.active_mask, rs);
-          acc = mfma16<XDT>(xf, w, acc);
+          acc = mfma16<XDT>(xf, wf[tt], acc);
         }
       }
-      issue(j);  // refill this slot with the item PF ahead
+      if (i0 + j + PF < n_items) issue(j);  // refill this slot with the item PF ahead (uniform)
       if (live && ++ct_c == CPT) {
         // tile done: park this wave's partial (rows m < M) in LDS
         ct_c = 0;
@@ -328,28 +397,37 @@ static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const Epilog
   // Each workgroup takes an equal share of the tiles and keeps the partial
   // sums of its whole share in LDS; when a share does not fit, the grid grows
   // until it does.
-  auto plan_for = [&](int per_cu, bool xlds, int* grid, int* share) -> bool {
-    const size_t fixed = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, 0);
+  auto plan_for = [&](int nslots, bool xlds, int* grid, int* share) -> bool {
+    const size_t fixed = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, 0, nslots);
     const size_t per_tile = (size_t)nw * M * 16 * sizeof(float);
-    const size_t avail = (size_t)kLdsMax / per_cu;
-    if (fixed + per_tile > avail) return false;
-    const int fit = (int)((avail - fixed) / per_tile);
-    int g = n_cu * per_cu < L.n_tiles ? n_cu * per_cu : L.n_tiles;
+    if (fixed + per_tile > (size_t)kLdsMax) return false;
+    const int fit = (int)(((size_t)kLdsMax - fixed) / per_tile);
+    int g = n_cu < L.n_tiles ? n_cu : L.n_tiles;
     const int min_grid = (L.n_tiles + fit - 1) / fit;
     if (g < min_grid) g = min_grid;
     *grid = g;
     *share = (L.n_tiles + g - 1) / g;
     return true;
   };
-  // One 8-wave workgroup per CU: measured faster than two co-resident ones
-  // (they contend for LDS gather bandwidth and stage the codebooks twice).
-  int grid = 0, share = 1;
+  // Two table slots when a workgroup's tiles can span two tables (several
+  // groups, or scaled tables with more than one scale run) and they fit with
+  // x in LDS; else one slot (a second table is restaged in the loop).
+  const bool segments = L.plan != nullptr || SCALED;
+  int grid = 0, share = 1, nslots = 0;
   bool xlds = true;
-  if (!plan_for(1, true, &grid, &share)) {
-    xlds = false;
-    if (!plan_for(1, false, &grid, &share)) return hipErrorInvalidValue;  // excluded by the host's eligibility check
+  for (const int ns : {2, 1}) {
+    if (ns == 2 && !segments) continue;
+    if (plan_for(ns, true, &grid, &share)) { nslots = ns; break; }
   }
-  const size_t lds = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, share);
+  if (nslots == 0) {
+    xlds = false;
+    for (const int ns : {2, 1}) {
+      if (ns == 2 && !segments) continue;
+      if (plan_for(ns, false, &grid, &share)) { nslots = ns; break; }
+    }
+  }
+  if (nslots == 0) return hipErrorInvalidValue;  // excluded by the host's eligibility check
+  const size_t lds = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, share, nslots);
   if (grid < 1) return hipSuccess;
   // one chunk per wave -> activation fragments stay in registers
   const int nchunk = (L.blocks_per_row + 63) / 64;
@@ -365,7 +443,7 @@ static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const Epilog
     attr_set[xmode] = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(nw * 64), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M,
-                     share);
+                     share, nslots);
   return hipGetLastError();
 }
 
@@ -375,7 +453,7 @@ static hipError_t decode_sem(const LayerArgs& L, const DtypeArgs& D, const Epilo
   if constexpr (S == 1) {
     // one stage: the row-scale product can be folded into the staged table
     // when every 16-row tile has a single scale value
-    const bool scaled = L.scale_rows % 16 == 0;
+    const bool scaled = L.scale_rows >= 16 && (L.scale_rows & (L.scale_rows - 1)) == 0;
     if (sem == SEM_FAST)
       return scaled ? decode_go<S, IdT, LM_A16, SEM_FAST, XDT, true>(L, D, E, x, M, n_cu, st)
                     : decode_go<S, IdT, LM_A16, SEM_FAST, XDT, false>(L, D, E, x, M, n_cu, st);

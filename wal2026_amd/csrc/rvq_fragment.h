@@ -37,6 +37,7 @@ struct FragTile {
   int32_t row0;      // first row inside the group
   int32_t rows;
   int32_t out_row0;  // first output row
+  int32_t grows;     // rows of the group
 };
 
 template <int S>
@@ -54,6 +55,7 @@ WAL_DEVICE FragTile<S> get_frag_tile(const LayerArgs& L, int t) {
     f.row0 = t * L.tile_rows;
     f.rows = min(L.tile_rows, L.g0.rows - f.row0);
     f.out_row0 = L.g0.row0 + f.row0;
+    f.grows = L.g0.rows;
   } else {
     typedef const __attribute__((address_space(1))) PlanHeader g_header_t;
     typedef const __attribute__((address_space(1))) PlanTile g_tile_t;
@@ -74,6 +76,7 @@ WAL_DEVICE FragTile<S> get_frag_tile(const LayerArgs& L, int t) {
     f.row0 = pt->row0;
     f.rows = pt->rows;
     f.out_row0 = pt->out_row0;
+    f.grows = G->rows;
   }
   return f;
 }
@@ -404,6 +407,52 @@ WAL_DEVICE f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) 
   } else {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                    c, 0, 0, 0);
+  }
+}
+
+
+// ---- staging from a codebook image ------------------------------------------
+// An image holds, per group, the S x K entries already in their LDS form (the
+// same bytes store_codebook_entry writes), so staging a group is a copy of
+// S * K * entry_bytes bytes in 16-byte pieces, batch by batch (8 pieces per
+// thread); SCALE_TABLE (16-bit entries) multiplies every staged fragment by
+// the row scale with the reference's rounding on the way.
+constexpr int kImageBatch = 8;
+
+WAL_DEVICE void load_image_batch(u32x4_t (&r)[kImageBatch], const uint8_t* img, int n16, int i0, int nt) {
+#pragma unroll
+  for (int u = 0; u < kImageBatch; ++u) r[u] = ldg128(img + (size_t)min(i0 + u * nt, n16 - 1) * 16);
+}
+
+template <int XDT, bool SCALE_TABLE>
+WAL_DEVICE void store_image_batch(uint8_t* lds, const u32x4_t (&r)[kImageBatch], int n16, int i0, int nt,
+                                  const RowScale& rs) {
+#pragma unroll
+  for (int u = 0; u < kImageBatch; ++u) {
+    const int i = i0 + u * nt;
+    if (i < n16) {
+      u32x4_t v = r[u];
+      if constexpr (SCALE_TABLE) v = scale_frag<XDT>(v, rs);
+      *reinterpret_cast<u32x4_t*>(lds + (size_t)i * 16) = v;
+    }
+  }
+}
+
+// Stage n16 pieces of an image into LDS; the first batch may already be in
+// `first` (issued early by the caller with i0 = threadIdx.x).
+template <int XDT, bool SCALE_TABLE>
+WAL_DEVICE void stage_image(uint8_t* lds, const uint8_t* img, int n16, const RowScale& rs,
+                            const u32x4_t (*first)[kImageBatch] = nullptr) {
+  const int nt = blockDim.x;
+  int i0 = threadIdx.x;
+  if (first != nullptr) {
+    store_image_batch<XDT, SCALE_TABLE>(lds, *first, n16, i0, nt, rs);
+    i0 += kImageBatch * nt;
+  }
+  for (; i0 < n16; i0 += kImageBatch * nt) {
+    u32x4_t r[kImageBatch];
+    load_image_batch(r, img, n16, i0, nt);
+    store_image_batch<XDT, SCALE_TABLE>(lds, r, n16, i0, nt, rs);
   }
 }
 

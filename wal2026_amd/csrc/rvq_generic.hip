@@ -7,7 +7,7 @@
 //    tile dequantised element by element.  Handles what the MFMA kernels do not
 //    (any block size, 32-bit ids, fp32 codebooks, block_scale, unaligned rows)
 //    and the Triton / route-codebook semantics.
-#include "rvq_kernels.h"
+#include "rvq_fragment.h"
 
 namespace wal {
 
@@ -219,6 +219,66 @@ hipError_t launch_generic_linear(const LayerArgs& L, const DtypeArgs& D, const E
     case SEM_ROUTE1: return generic_dt<SEM_ROUTE1>(L, D, E, x, M, st);
     default: return generic_dt<SEM_RECON>(L, D, E, x, M, st);
   }
+}
+
+
+// ---------------------------------------------------------------------------
+// Codebook image: every entry of every stage of every group converted once
+// into the form the MFMA kernels stage in LDS (store_codebook_entry, the same
+// code the kernels run when they convert raw codebooks themselves).  One
+// thread per entry.
+// ---------------------------------------------------------------------------
+template <int LMODE, int SEM, int XDT>
+__global__ __launch_bounds__(256) void rvq_image_kernel(LayerArgs L, DtypeArgs D, uint8_t* __restrict__ dst) {
+  const int S = L.num_stages, K = L.codebook_size;
+  const int64_t per_group = (int64_t)S * K;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= per_group * L.n_groups) return;
+  const int g = (int)(e / per_group);
+  const int rem = (int)(e - (int64_t)g * per_group);
+  const int s = rem / K;
+  const int k = rem - s * K;
+  const void* cbp;
+  const void* ssp;
+  if (L.plan == nullptr) {
+    cbp = L.g0.codebooks[s];
+    ssp = L.g0.stage_scales;
+  } else {
+    typedef const __attribute__((address_space(1))) wal_rvq_group g_group_t;
+    const __attribute__((address_space(1))) char* base = (const __attribute__((address_space(1))) char*)(L.plan);
+    g_group_t* G = (g_group_t*)(base + ((const __attribute__((address_space(1))) PlanHeader*)base)->groups_offset) + g;
+    cbp = G->codebooks[s];
+    ssp = G->stage_scales;
+  }
+  const char* cb = static_cast<const char*>(cbp);
+  u32x4_t raw[2];
+  if (D.cb_dtype == WAL_F32) {
+    raw[0] = ldg128(cb + (size_t)k * 32);
+    raw[1] = ldg128(cb + (size_t)k * 32 + 16);
+  } else {
+    raw[0] = ldg128(cb + (size_t)k * 16);
+    raw[1] = u32x4_t{0, 0, 0, 0};
+  }
+  const bool has_ss = ssp != nullptr;
+  const float ss = has_ss ? load_f(ssp, D.sc_dtype, s) : 1.0f;
+  store_codebook_entry<LMODE, SEM, XDT, false>(dst + (size_t)g * per_group * lds_entry_bytes<LMODE>(), rem, s, raw,
+                                               D.cb_dtype, has_ss, ss, RowScale{0.0f, 0u, 0u});
+}
+
+template <int LMODE, int SEM>
+static hipError_t image_x(const LayerArgs& L, const DtypeArgs& D, void* dst, hipStream_t st) {
+  const int64_t n = (int64_t)L.n_groups * L.num_stages * L.codebook_size;
+  dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  uint8_t* d = static_cast<uint8_t*>(dst);
+  if (D.x_dtype == WAL_BF16) hipLaunchKernelGGL((rvq_image_kernel<LMODE, SEM, WAL_BF16>), grid, block, 0, st, L, D, d);
+  else hipLaunchKernelGGL((rvq_image_kernel<LMODE, SEM, WAL_F16>), grid, block, 0, st, L, D, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_image(const LayerArgs& L, const DtypeArgs& D, int sem, int lmode, void* dst, hipStream_t st) {
+  if (lmode == LM_A16) return sem == SEM_FAST ? image_x<LM_A16, SEM_FAST>(L, D, dst, st) : image_x<LM_A16, SEM_RECON>(L, D, dst, st);
+  if (lmode == LM_H16) return image_x<LM_H16, SEM_RECON>(L, D, dst, st);
+  return image_x<LM_F32, SEM_RECON>(L, D, dst, st);
 }
 
 }  // namespace wal

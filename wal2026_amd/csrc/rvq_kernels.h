@@ -63,6 +63,9 @@ hipError_t launch_generic_linear(const LayerArgs& L, const DtypeArgs& D, const E
 // capi.hip decides when those kernels apply (mfma_eligible).
 enum LdsMode : int { LM_A16 = 0, LM_H16 = 1, LM_F32 = 2 };
 
+// Codebook image of every group in LdsMode form (rvq_generic.hip).
+hipError_t launch_image(const LayerArgs& L, const DtypeArgs& D, int sem, int lmode, void* dst, hipStream_t st);
+
 template <int XDT, typename IdT>
 hipError_t decode_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
                         const void* x, int M, int n_cu, hipStream_t st);

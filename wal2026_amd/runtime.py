@@ -163,6 +163,32 @@ class _LayerDesc:
             L.plan = self.plan.data_ptr()
         self.device = device
         self.key = _desc_key(groups)
+        self.fused_ok = g0.block_size == 8 and S <= 4
+        self._calls: dict[tuple[int, int], _lib.WalLayer] = {}
+        self._images: dict[tuple[int, int], Tensor] = {}
+
+    def layer_for(self, semantics: int, x_dtype: torch.dtype) -> "_lib.WalLayer":
+        """The wal_rvq_layer for a linear call: the base descriptor plus the
+        codebook image for this semantics and activation dtype, built on the
+        device the first time (wal_rvq_image_build) and cached here, like the
+        reference's derived codebook caches (src/runtime.py:431-448)."""
+        xtag = _lib.FLOAT_DTYPES.get(x_dtype)
+        key = (semantics, -1 if xtag is None else xtag)
+        call = self._calls.get(key)
+        if call is None:
+            call = _lib.WalLayer.from_buffer_copy(self.layer)
+            if self.fused_ok and x_dtype in (torch.float16, torch.bfloat16):
+                lib = _lib.lib()
+                size = ctypes.c_size_t(0)
+                if lib.wal_rvq_image_size(ctypes.byref(self.layer), semantics, xtag, ctypes.byref(size)) == _lib.OK:
+                    img = torch.empty(size.value, dtype=torch.uint8, device=self.device)
+                    _lib.check(lib.wal_rvq_image_build(ctypes.byref(self.layer), semantics, xtag, img.data_ptr(),
+                                                       size.value, _lib.stream_ptr(self.device)))
+                    call.image = img.data_ptr()
+                    call.image_tag = _lib.image_tag(semantics, xtag)
+                    self._images[key] = img
+            self._calls[key] = call
+        return call
 
 
 _SCALE_RUNS = (128, 64, 32, 16)
@@ -254,6 +280,16 @@ class PackedBlockRVQGroup(nn.Module):
         self._desc = None
         self._triton_stage_ids = self._triton_codebooks = None
         return super()._apply(fn, recurse)
+
+    def invalidate_caches(self) -> None:
+        """Drop the device descriptor, id-range check and codebook images
+        (rebuilt on the next call).  Needed after changing buffers in place."""
+        self._desc = None
+        self._triton_stage_ids = self._triton_codebooks = None
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self.invalidate_caches()  # load_state_dict copies into the buffers in place
+        return super()._load_from_state_dict(*args, **kwargs)
 
     def _stage_tensors(self) -> list[tuple[Tensor, Tensor]]:
         return [(getattr(self, f"stage_ids_{i}"), getattr(self, f"codebook_{i}")) for i in range(self.num_stages)]
@@ -413,6 +449,18 @@ class PackedGroupedBlockRVQLinear(nn.Module):
         self._desc = None
         return super()._apply(fn, recurse)
 
+    def invalidate_caches(self) -> None:
+        """Drop the cached descriptors and codebook images of the layer and
+        its groups (rebuilt on the next call); needed after changing buffers in
+        place."""
+        self._desc = None
+        for g in self.groups:
+            g.invalidate_caches()
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self._desc = None  # the groups reset their own caches
+        return super()._load_from_state_dict(*args, **kwargs)
+
     def _descriptor(self) -> _LayerDesc:
         dev = self.groups[0].row_scale.device
         groups = list(self.groups)
@@ -468,13 +516,14 @@ class PackedGroupedBlockRVQLinear(nn.Module):
                 part = torch.empty(M, r1 - r0, dtype=y.dtype, device=dev)
                 d = g._descriptor()
                 b = None if bias is None else bias[r0:r1].contiguous()
-                _lib.check(lib.wal_rvq_linear(ctypes.byref(d.layer), sem, g.active_stage_mask(), x_c.data_ptr(), M,
+                _lib.check(lib.wal_rvq_linear(ctypes.byref(d.layer_for(sem, x_c.dtype)), sem, g.active_stage_mask(),
+                                              x_c.data_ptr(), M,
                                               _lib.float_tag(x_c.dtype), _ptr(b), btag, part.data_ptr(),
                                               _lib.float_tag(y.dtype), stream))
                 y[:, r0:r1] = part
             return y
         desc = self._descriptor()
-        _lib.check(lib.wal_rvq_linear(ctypes.byref(desc.layer), sem, mask, x_c.data_ptr(), M,
+        _lib.check(lib.wal_rvq_linear(ctypes.byref(desc.layer_for(sem, x_c.dtype)), sem, mask, x_c.data_ptr(), M,
                                       _lib.float_tag(x_c.dtype), _ptr(bias), btag, y.data_ptr(),
                                       _lib.float_tag(y.dtype), stream))
         return y
@@ -531,7 +580,8 @@ class _GroupView:
         if x_c.shape[0] == 0:
             return y
         d = g._descriptor()
-        _lib.check(_lib.lib().wal_rvq_linear(ctypes.byref(d.layer), _lib.RECONSTRUCT, 0, x_c.data_ptr(),
+        _lib.check(_lib.lib().wal_rvq_linear(ctypes.byref(d.layer_for(_lib.RECONSTRUCT, x_c.dtype)), _lib.RECONSTRUCT,
+                                             0, x_c.data_ptr(),
                                              x_c.shape[0], _lib.float_tag(x_c.dtype), None, _lib.F32, y.data_ptr(),
                                              _lib.float_tag(y.dtype), _lib.stream_ptr(dev)))
         return y
