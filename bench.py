@@ -6,8 +6,11 @@ gate/up (14336 x 4096) and down (4096 x 14336), each a single-stage Block-RVQ
 layer with a 4096-entry fp16 codebook, 16-bit indices and an fp16 scale shared
 by 128-row groups, bf16 activations.  Weights are seeded random (synthetic,
 no checkpoint); all 224 linears live in HBM at once (1.76 GB of indices), so
-every step streams cold compressed bytes.  The step is captured in a HIP graph
-and replayed; the timed region is exactly --steps replays.
+every step streams cold compressed bytes.  Linears of a layer that read the
+same activation run as one launch (q/k/v, gate/up: FusedBlockRVQLinears), the
+others one launch each; the drop-in step with one launch per linear is timed
+too and reported as config.unfused_tok_s.  Each step is captured in a HIP
+graph and replayed; the timed region is exactly --steps replays.
 
 Prints one JSON line (metric, value in tok/s, roofline of the dominant kernel
 measured live with HIP events, CPU baseline of the reference's per_group op
@@ -29,9 +32,11 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from wal2026_amd import PackedGroupedBlockRVQLinear, synth  # noqa: E402
+from wal2026_amd import FusedBlockRVQLinears, PackedGroupedBlockRVQLinear, synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+# linears of a layer that read the same activation, fused into one launch
+FUSION_GROUPS = (("qkv", ("q_proj", "k_proj", "v_proj")), ("gate_up", ("gate_proj", "up_proj")))
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 
 
@@ -59,8 +64,8 @@ def linear_bytes(cfg: synth.Config, n: int, k: int) -> int:
     return cfg.num_stages * n * B * ib + G * cfg.num_stages * cfg.codebook_size * cfg.block_size * 2 + n * 2
 
 
-def time_kernel_family(stack, name, x, reps: int = 3) -> float:
-    """Average GPU duration (us) of one launch of `name`.
+def time_kernel_family(mods, x, reps: int = 3) -> float:
+    """Average GPU duration (us) of one launch of a module (one per layer).
 
     The launches (one per layer, so each reads weights the previous one did
     not) are queued behind a GPU sleep, so the host enqueues all of them before
@@ -73,16 +78,30 @@ def time_kernel_family(stack, name, x, reps: int = 3) -> float:
         torch.cuda.synchronize()
         torch.cuda._sleep(20_000_000)  # ~10 ms of GPU spin: the queue fills behind it
         pairs = []
-        for layer in stack:
+        for mod in mods:
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record(stream)
-            layer[name](x)
+            mod(x)
             b.record(stream)
             pairs.append((a, b))
         torch.cuda.synchronize()
         times.extend(a.elapsed_time(b) * 1000.0 for a, b in pairs)
     return sum(times) / len(times)
+
+
+def traffic_bytes(path: str):
+    """HBM bytes per launch of the dominant kernel from a committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, already scaled by the copy-kernel
+    calibration factor the summary states); None when there is none."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(cfg: synth.Config, budget_s: float = 20.0) -> dict:
@@ -135,6 +154,8 @@ def main() -> int:
     ap.add_argument("--m", type=int, default=1)
     ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-summary", default=str(ROOT / "profiles" / "decode_c3_gate_up_pmc.txt"),
+                    help="rocprofv3 --pmc summary giving the dominant kernel's HBM traffic (optional)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (the path has no multi-GPU code); "
@@ -154,45 +175,73 @@ def main() -> int:
     gen = synth.generator(1, dev)
     xs = {k: synth.make_activation(cfg.m, k, cfg.x_dtype, gen, dev) for k in {k for _, _, k in cfg.shapes()}}
 
-    def step():
+    # drop-in step: every linear its own launch (the reference's call pattern)
+    def step_unfused():
         for layer in stack:
             for name, _n, k in cfg.shapes():
                 layer[name](xs[k])
 
-    step()  # builds every layer's descriptor outside the graph
-    torch.cuda.synchronize()
-    log("capturing one step in a HIP graph")
-    graph = torch.cuda.CUDAGraph()
-    cap_stream = torch.cuda.Stream()
-    cap_stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(cap_stream):
-        step()
-    torch.cuda.current_stream().wait_stream(cap_stream)
-    torch.cuda.synchronize()
-    with torch.cuda.graph(graph):
-        step()
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    log(f"timing {args.steps} graph replays")
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        graph.replay()
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1000.0 / args.steps
+    # fused step: linears that read the same activation share one launch
+    names = [n for n, _, _ in cfg.shapes()]
+    fuse = [(f, members) for f, members in FUSION_GROUPS if all(m in names for m in members)]
+    fused_members = {m for _, members in fuse for m in members}
+    for layer in stack:
+        for f, members in fuse:
+            layer[f] = FusedBlockRVQLinears([layer[m] for m in members])
+    shape = {n: (o, k) for n, o, k in cfg.shapes()}
+
+    def fused_launches():
+        """(name, in_features, compressed bytes) of the fused step's launches."""
+        out = [(f, shape[members[0]][1], sum(linear_bytes(cfg, *shape[m]) for m in members)) for f, members in fuse]
+        out += [(n, k, linear_bytes(cfg, o, k)) for n, o, k in cfg.shapes() if n not in fused_members]
+        return out
+
+    def step_fused():
+        for layer in stack:
+            for name, k, _b in fused_launches():
+                layer[name](xs[k])
+
+    def graph_ms(step) -> float:
+        step()  # builds descriptors and codebook images outside the graph
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1000.0 / args.steps
+
+    log(f"timing {args.steps} graph replays of the drop-in step (one launch per linear)")
+    ms_unfused = graph_ms(step_unfused)
+    log(f"timing {args.steps} graph replays of the fused step ({len(fused_launches())} launches per layer)")
+    ms_per_step = graph_ms(step_fused)
     tok_s = cfg.m * 1000.0 / ms_per_step
     us_per_layer = ms_per_step * 1000.0 / layers
 
-    # dominant kernel: the largest linear's decode launch, timed per launch
-    dom_name, dom_n, dom_k = max(cfg.shapes(), key=lambda s: s[1] * s[2])
-    log(f"timing the dominant kernel ({dom_name}, {dom_n}x{dom_k}) per launch")
-    dom_us = time_kernel_family(stack, dom_name, xs[dom_k])
-    dom_bytes = linear_bytes(cfg, dom_n, dom_k)
+    # dominant kernel: the fused step's largest launch, timed per launch
+    dom_name, dom_k, dom_bytes = max(fused_launches(), key=lambda t: t[2])
+    log(f"timing the dominant kernel ({dom_name}) per launch")
+    dom_us = time_kernel_family([layer[dom_name] for layer in stack], xs[dom_k])
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    per_launch = {}
+    for name, k, nbytes in fused_launches():
+        us = time_kernel_family([layer[name] for layer in stack], xs[k], reps=1)
+        per_launch[name] = {"us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
     per_linear = {}
     for name, n, k in cfg.shapes():
-        us = time_kernel_family(stack, name, xs[k], reps=1)
+        us = time_kernel_family([layer[name] for layer in stack], xs[k], reps=1)
         per_linear[name] = {"us": round(us, 3), "GBps": round(linear_bytes(cfg, n, k) / (us * 1e-6) / 1e9, 1)}
     layer_bytes = cfg.compressed_bytes_per_layer()
 
@@ -213,24 +262,28 @@ def main() -> int:
             "workload": f"{cfg.name}: Llama-3-8B-shaped {layers}-layer stack of compressed linears, "
                         f"S={cfg.num_stages}, K={cfg.codebook_size}, d={cfg.block_size}, "
                         f"{str(cfg.ids_dtype()).replace('torch.', '')} ids, scale per {cfg.scale_rows} rows, "
-                        f"decode M={cfg.m}, one HIP graph per step",
+                        f"decode M={cfg.m}, one HIP graph per step; linears sharing an input fused "
+                        f"({', '.join(f for f, _ in fuse)})",
             "layers": layers,
             "m": cfg.m,
             "us_per_layer": round(us_per_layer, 3),
             "compressed_bytes_per_layer": layer_bytes,
             "step_hbm_fraction": round(layer_bytes * layers / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "per_linear": per_linear,
+            "unfused_tok_s": round(cfg.m * 1000.0 / ms_unfused, 3),
+            "unfused_us_per_layer": round(ms_unfused * 1000.0 / layers, 3),
+            "per_launch": per_launch,
+            "per_linear_unfused": per_linear,
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"rvq_decode_kernel ({dom_name} {dom_n}x{dom_k})",
+            "kernel": f"rvq_decode_kernel ({dom_name}, {dom_bytes} compressed bytes)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "avg_launch_us": round(dom_us, 3),
             "algorithmic_bytes_per_launch": dom_bytes,
-            "traffic": None,
+            "traffic": traffic_bytes(args.pmc_summary),
         },
     }
     if not args.no_cpu_baseline:

@@ -21,6 +21,7 @@ from .runtime import (
     TARGET_LINEAR_SUFFIXES,
     AdaptiveFusedIDRouteLinear,
     CachedPackedIDRouteLinear,
+    FusedBlockRVQLinears,
     FusedIDRouteLinear,
     PackedBlockRVQGroup,
     PackedGroupedBlockRVQLinear,
@@ -36,6 +37,7 @@ __all__ = [
     "AdaptiveFusedIDRouteLinear",
     "BlockRVQEncoding",
     "CachedPackedIDRouteLinear",
+    "FusedBlockRVQLinears",
     "FusedIDRouteLinear",
     "GroupedBlockRVQEncoding",
     "PackedBlockRVQGroup",

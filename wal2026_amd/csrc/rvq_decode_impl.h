@@ -149,6 +149,11 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
                                                                        const uint16_t* __restrict__ x, int M,
                                                                        int max_tiles, int nslots) {
   static_assert(!SCALED || LMODE == LM_A16, "scaled tables hold one 16-bit value per element");
+  // Touch every cache line of the kernel arguments at once: otherwise the
+  // compiler loads each field where it is first used, and every first touch
+  // of a line is its own dependent scalar-memory round trip.
+  asm volatile("" ::"s"(L.in_features), "s"(L.plan), "s"(L.g0.stage_ids[0]), "s"(L.g0.codebooks[4]),
+               "s"(L.g0.row_scale), "s"(L.image), "s"(D.x_dtype), "s"(E.y), "s"(E.bias_mode), "s"(x), "s"(nslots));
   constexpr bool XLDS = XMODE != XM_GLOBAL;
   constexpr int PF = decode_prefetch<S, IdT>(), NV = sizeof(IdT);
   constexpr int ESZ = lds_entry_bytes<LMODE>();
@@ -184,11 +189,47 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   // other value inside the LDS allocation (next power of two of K entries).
   const uint32_t kmask = K <= 1 ? 0u : (0xffffffffu >> __builtin_clz((uint32_t)(K - 1)));
 
+  // ---- prologue, part 1: loads of the activations and tables ---------------
+  // The range's tiles fall in one or two table segments (same group and, for
+  // scaled tables, same scale run): the segment boundary is where the first
+  // tile's group or scale run ends.  Both segments' tables are staged into
+  // slots 0 and 1 (when the launch has two); any other segment (a range
+  // longer than a group, or a single slot) is restaged in the loop.  These
+  // loads are issued before the index ring, so waiting for them (vmcnt is
+  // in order) does not wait for the cold index loads behind them.
+  FragTile<S> cti = tile_at<S>(L, t_begin);
+  int seg1 = t_begin + (cti.grows - cti.row0 + 15) / 16;  // first tile of the next group
+  if constexpr (SCALED) {
+    const int run_left = L.scale_rows - (cti.row0 & (L.scale_rows - 1));  // scale_rows: power of two >= 16
+    seg1 = min(seg1, t_begin + run_left / 16);
+  }
+  const bool two = seg1 < t_end && nslots == 2;
+  FragTile<S> sti = two ? tile_at<S>(L, seg1) : cti;
+  int key[2] = {table_key<S, SCALED>(L, cti), two ? table_key<S, SCALED>(L, sti) : -1};
+  const bool have_image = L.image != nullptr;
+  const uint8_t* img0 = have_image ? L.image + (size_t)cti.group * tbl_bytes : nullptr;
+  const uint8_t* img1 = have_image ? L.image + (size_t)sti.group * tbl_bytes : nullptr;
+  const int n16 = XLDS ? M * in / 8 : 0;  // 16-byte pieces of x (in % 128 == 0)
+  const int t16 = tbl_bytes / 16;
+  u32x4_t xr[XR];
+#pragma unroll
+  for (int u = 0; u < XR; ++u) xr[u] = ldg128(x + (size_t)min(tid + u * (int)blockDim.x, max(n16 - 1, 0)) * 8);
+  u32x4_t b0[kImageBatch], b1[kImageBatch];
+  if (have_image) {
+    load_image_batch(b0, img0, t16, tid, blockDim.x);
+    if (two) load_image_batch(b1, img1, t16, tid, blockDim.x);
+  }
+  uint32_t sc0 = 0, sc1 = 0;  // scales of the two segments (scaled tables)
+  if constexpr (SCALED) {
+    sc0 = ldg<uint16_t>(cti.p.row_scale, scale_index(L, cti.row0));
+    sc1 = ldg<uint16_t>(sti.p.row_scale, scale_index(L, sti.row0));
+  }
+
   // ---- index ring: issue cursor runs PF items ahead of the compute cursor ----
   u32x4_t ring[PF][S][NV];
   uint32_t rsr[PF];  // raw bits of the lane's row scale for the slot's tile
   int is_t = 0, is_c = 0;
-  FragTile<S> iti = tile_at<S>(L, t_begin);
+  FragTile<S> iti = cti;
   auto issue = [&](int j) {
     // Always issues the same buffer loads (straight-line code); a slot past
     // the range, or a chunk past the row, gets an out-of-range offset and
@@ -216,52 +257,18 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
 #pragma unroll
   for (int j = 0; j < PF; ++j) issue(j);
 
-  // ---- prologue: one memory round trip for activations and tables -----------
-  // The range's tiles fall in one or two table segments (same group and, for
-  // scaled tables, same scale run): the segment boundary is where the first
-  // tile's group or scale run ends.  Both segments' tables are staged now,
-  // into slots 0 and 1; a third segment (rare: a range longer than a group)
-  // is restaged in the loop.
-  FragTile<S> cti = tile_at<S>(L, t_begin);
-  int seg1 = t_begin + (cti.grows - cti.row0 + 15) / 16;  // first tile of the next group
-  if constexpr (SCALED) {
-    const int run_left = L.scale_rows - (cti.row0 & (L.scale_rows - 1));  // scale_rows: power of two >= 16
-    seg1 = min(seg1, t_begin + run_left / 16);
-  }
-  const bool two = seg1 < t_end && nslots == 2;
-  FragTile<S> sti = two ? tile_at<S>(L, seg1) : cti;
-  int key[2] = {table_key<S, SCALED>(L, cti), two ? table_key<S, SCALED>(L, sti) : -1};
-  const uint8_t* img0 = L.image != nullptr ? L.image + (size_t)cti.group * tbl_bytes : nullptr;
-  const uint8_t* img1 = L.image != nullptr ? L.image + (size_t)sti.group * tbl_bytes : nullptr;
-  const int n16 = XLDS ? M * in / 8 : 0;  // 16-byte pieces of x (in % 128 == 0)
-  u32x4_t xr[XR];
-#pragma unroll
-  for (int u = 0; u < XR; ++u) xr[u] = ldg128(x + (size_t)min(tid + u * (int)blockDim.x, max(n16 - 1, 0)) * 8);
+  // ---- prologue, part 2: stage the tables and x while the ring loads fly ---
   if (tid < 16) reinterpret_cast<u32x4_t*>(zrow)[tid] = u32x4_t{0, 0, 0, 0};
-  uint32_t sc1 = 0;
-  if (L.image != nullptr) {
-    // first batches of both tables issued before the scales are read, so all
-    // the prologue's loads share one round trip
-    const int t16 = tbl_bytes / 16;
-    u32x4_t b0[kImageBatch], b1[kImageBatch];
-    load_image_batch(b0, img0, t16, tid, blockDim.x);
-    if (two) load_image_batch(b1, img1, t16, tid, blockDim.x);
-    if constexpr (SCALED) sc1 = two ? (uint32_t)ldg<uint16_t>(sti.p.row_scale, scale_index(L, sti.row0)) : 0u;
-    RowScale r0 = make_row_scale<XDT>(0.0f), r1 = r0;
-    if constexpr (SCALED) {
-      r0 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(rsr[0]), D.sc_dtype));
-      r1 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(sc1), D.sc_dtype));
-    }
+  RowScale r0 = make_row_scale<XDT>(0.0f), r1 = r0;
+  if constexpr (SCALED) {
+    r0 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(sc0), D.sc_dtype));
+    r1 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(sc1), D.sc_dtype));
+  }
+  if (have_image) {
     stage_image<XDT, SCALED>(lds_cb, img0, t16, r0, &b0);
     if (two) stage_image<XDT, SCALED>(lds_cb + tbl_bytes, img1, t16, r1, &b1);
   } else {
     // no image: convert the raw codebooks here (out of line)
-    RowScale r0 = make_row_scale<XDT>(0.0f), r1 = r0;
-    if constexpr (SCALED) {
-      sc1 = two ? (uint32_t)ldg<uint16_t>(sti.p.row_scale, scale_index(L, sti.row0)) : 0u;
-      r0 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(rsr[0]), D.sc_dtype));
-      r1 = make_row_scale<XDT>(scale_bits_to_f32(__builtin_amdgcn_readfirstlane(sc1), D.sc_dtype));
-    }
     stage_table<S, LMODE, SEM, XDT, SCALED>(0u, nullptr, cti.p, K, D, r0);
     if (two) stage_table<S, LMODE, SEM, XDT, SCALED>((uint32_t)tbl_bytes, nullptr, sti.p, K, D, r1);
   }

@@ -563,6 +563,101 @@ class PackedGroupedBlockRVQLinear(nn.Module):
         return out.reshape(*orig[:-1], self.out_features)
 
 
+class FusedBlockRVQLinears(nn.Module):
+    """Several PackedGroupedBlockRVQLinear layers that read the same input
+    (q/k/v, gate/up of TARGET_LINEAR_SUFFIXES) run as ONE launch.
+
+    Their row groups become one multi-group layer whose output rows are the
+    linears' outputs side by side; ``forward(x)`` returns one output per
+    linear (views of one [..., sum(out_features)] tensor), each equal to what
+    that linear's own forward returns (the same arithmetic per row).  The
+    reference has no counterpart: it calls each linear separately
+    (src/runtime.py:1362); fusing saves the per-launch latency and codebook
+    staging of the small linears.  The linears stay owned by the model; this
+    module only holds references.
+    """
+
+    def __init__(self, linears) -> None:
+        super().__init__()
+        linears = list(linears)
+        if not linears:
+            raise ValueError("nothing to fuse")
+        in_f = linears[0].in_features
+        kinds = set()
+        for lin in linears:
+            if not isinstance(lin, PackedGroupedBlockRVQLinear):
+                raise TypeError(f"cannot fuse {type(lin).__name__}")
+            if lin.in_features != in_f:
+                raise ValueError("fused linears must share in_features")
+            kinds.add("fast" if lin.matmul_strategy in _FAST_STRATEGIES else
+                      "recon" if lin.matmul_strategy in _RECON_STRATEGIES else lin.matmul_strategy)
+        if len(kinds) != 1 or not kinds <= {"fast", "recon"}:
+            raise ValueError(f"fused linears must all use reconstruct_weight or all reconstruct_weight_fast "
+                             f"strategies (got {sorted(kinds)})")
+        self._fast = kinds == {"fast"}
+        self._linears = linears  # plain list: not submodules
+        self.in_features = in_f
+        self.out_features = [lin.out_features for lin in linears]
+        self._desc: _LayerDesc | None = None
+        self._bias: Tensor | None = None
+
+    def _groups_and_slices(self):
+        groups, slices, base = [], [], 0
+        for lin in self._linears:
+            for (r0, r1), g in zip(lin.row_slices, lin.groups):
+                groups.append(g)
+                slices.append((base + r0, base + r1))
+            base += lin.out_features
+        return groups, slices, base
+
+    def _descriptor(self) -> _LayerDesc:
+        groups, slices, total = self._groups_and_slices()
+        dev = groups[0].row_scale.device
+        if self._desc is None or self._desc.device != dev or self._desc.key != _desc_key(groups):
+            self._desc = _LayerDesc(groups, slices, self.in_features, total, dev)
+            biases = [lin.bias for lin in self._linears]
+            if any(b is not None for b in biases):
+                self._bias = torch.cat([b if b is not None else torch.zeros(n, dtype=torch.bfloat16, device=dev)
+                                        for b, n in zip(biases, self.out_features)]).contiguous()
+            else:
+                self._bias = None
+        return self._desc
+
+    def invalidate_caches(self) -> None:
+        self._desc = None
+        self._bias = None
+
+    def forward(self, x: Tensor) -> tuple[Tensor, ...]:
+        orig = x.shape
+        x_flat = x.reshape(-1, orig[-1])
+        dev = _lib.require_rocm(x_flat, self._linears[0].groups[0].row_scale)
+        x_c = x_flat.contiguous()
+        if x_c.data_ptr() % 16:
+            x_c = x_c.clone()
+        desc = self._descriptor()
+        total = sum(self.out_features)
+        M = x_c.shape[0]
+        y = torch.empty(M, total, dtype=x_flat.dtype, device=dev)
+        if M:
+            sem = _lib.RECONSTRUCT_FAST if self._fast else _lib.RECONSTRUCT
+            mask = 0
+            if self._fast:
+                masks = {g.active_stage_mask() for lin in self._linears for g in lin.groups}
+                if len(masks) != 1:
+                    raise ValueError("fused reconstruct_weight_fast linears must decode the same stages")
+                mask = masks.pop()
+            bias = self._bias
+            _lib.check(_lib.lib().wal_rvq_linear(
+                ctypes.byref(desc.layer_for(sem, x_c.dtype)), sem, mask, x_c.data_ptr(), M, _lib.float_tag(x_c.dtype),
+                _ptr(bias), _lib.float_tag(bias.dtype) if bias is not None else _lib.F32, y.data_ptr(),
+                _lib.float_tag(y.dtype), _lib.stream_ptr(dev)))
+        outs, o0 = [], 0
+        for n in self.out_features:
+            outs.append(y[:, o0:o0 + n].reshape(*orig[:-1], n))
+            o0 += n
+        return tuple(outs)
+
+
 class _GroupView:
     """One group as a single-group layer without bias (for per-group calls)."""
 
