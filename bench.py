@@ -154,6 +154,9 @@ def main() -> int:
     ap.add_argument("--m", type=int, default=1)
     ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
+                    help="only run the dominant launch N times per layer, then one 256 MiB device copy "
+                         "(the calibration kernel); for rocprofv3 --pmc runs")
     ap.add_argument("--pmc-summary", default=str(ROOT / "profiles" / "decode_c3_gate_up_pmc.txt"),
                     help="rocprofv3 --pmc summary giving the dominant kernel's HBM traffic (optional)")
     args = ap.parse_args()
@@ -222,6 +225,22 @@ def main() -> int:
             graph.replay()
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) * 1000.0 / args.steps
+
+    if args.profile_dominant:
+        step_fused()  # descriptors and codebook images
+        torch.cuda.synchronize()
+        dom_name, dom_k, dom_bytes = max(fused_launches(), key=lambda t: t[2])
+        for _ in range(args.profile_dominant):
+            for layer in stack:
+                layer[dom_name](xs[dom_k])
+        torch.cuda.synchronize()
+        src = torch.empty(64 * 2**20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # 256 MiB read + 256 MiB written: the counters' calibration
+        torch.cuda.synchronize()
+        print(json.dumps({"profiled": dom_name, "launches": args.profile_dominant * layers,
+                          "algorithmic_bytes_per_launch": dom_bytes, "calibration_copy_bytes": 2**28}), flush=True)
+        return 0
 
     log(f"timing {args.steps} graph replays of the drop-in step (one launch per linear)")
     ms_unfused = graph_ms(step_unfused)
