@@ -60,7 +60,15 @@ typedef enum wal_rvq_semantics {
   /* PackedBlockRVQGroup.reconstruct_weight_fast (src/runtime.py:568-598):
    * arithmetic in the output dtype over the active stages only.  Used by
    * per_group_fast / full_weight_fast (:1371-1376, :1491-1500). */
-  WAL_RVQ_RECONSTRUCT_FAST = 1
+  WAL_RVQ_RECONSTRUCT_FAST = 1,
+  /* PackedBlockRVQGroup.stagewise_block_matmul (src/runtime.py:878-894),
+   * strategy stagewise_einsum (:1466-1475): per stage, codewords cast to the
+   * x dtype (times the stage scale cast to it), contracted and rounded to the
+   * x dtype, the stage results summed in the x dtype from +0 over all stages,
+   * then times row_scale cast to the x dtype; a bias is added to that rounded
+   * result.  wal_rvq_linear only (there is no dense weight); groups with a
+   * block_scale are refused (src/runtime.py:837-846). */
+  WAL_RVQ_STAGEWISE = 2
 } wal_rvq_semantics;
 
 /* The buffers of one PackedBlockRVQGroup (src/runtime.py:249-290), device

@@ -69,6 +69,9 @@ def lib() -> ctypes.CDLL:
         L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.or_reconstruct_weight.restype = ctypes.c_int
         L.or_reconstruct_weight.argtypes = [ctypes.POINTER(_Group), ctypes.c_int, ctypes.c_void_p]
+        L.or_stagewise_linear.restype = ctypes.c_int
+        L.or_stagewise_linear.argtypes = [ctypes.POINTER(_Group), ctypes.c_void_p, ctypes.c_int, ctypes.c_int64,
+                                          ctypes.c_void_p]
         L.or_reconstruct_weight_fast.restype = ctypes.c_int
         L.or_reconstruct_weight_fast.argtypes = [ctypes.POINTER(_Group), ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]
         L.or_linear_f64.restype = None
@@ -167,6 +170,16 @@ def reconstruct_weight_fast(g: OracleGroup, active_stages, out_dtype: torch.dtyp
     if rc != 0:
         raise ValueError(f"or_reconstruct_weight_fast failed ({rc})")
     return out
+
+
+def stagewise_linear(g: OracleGroup, x: torch.Tensor) -> torch.Tensor:
+    """stagewise_block_matmul of one group (src/runtime.py:878-894), y in x dtype."""
+    x = _cpu(x)
+    y = torch.empty(x.shape[0], g.rows, dtype=x.dtype)
+    rc = lib().or_stagewise_linear(ctypes.byref(g.struct), x.data_ptr(), _FLOAT_TAG[x.dtype], x.shape[0], y.data_ptr())
+    if rc != 0:
+        raise ValueError(f"or_stagewise_linear failed ({rc})")
+    return y
 
 
 def linear_f64(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:

@@ -85,6 +85,22 @@ def per_group_forward(x, groups, row_slices, out_features, bias=None):
     return torch.cat(parts, dim=-1).reshape(*lead, out_features)
 
 
+def stagewise_block_matmul(x, stage_ids, codebooks, row_scale, in_features, stage_scales=None):
+    """src/runtime.py:878-894: per stage an einsum in x dtype, summed in x dtype."""
+    rows, bpr = stage_ids[0].shape
+    d = codebooks[0].shape[1]
+    pad = bpr * d - in_features
+    xb = (F.pad(x, (0, pad), value=0.0) if pad else x).reshape(-1, bpr, d)   # :881-885
+    out = torch.zeros((xb.shape[0], rows), dtype=xb.dtype)                  # :886
+    ss = None if stage_scales is None else stage_scales.to(xb.dtype)        # :887
+    for s, (ids, cb) in enumerate(zip(stage_ids, codebooks)):
+        blocks = cb[ids.reshape(-1).long()].view(rows, bpr, d).to(xb.dtype)  # :889
+        if ss is not None:
+            blocks = blocks * ss[s]                                          # :891
+        out = out + torch.einsum("mbd,rbd->mr", xb, blocks)                  # :892
+    return out * row_scale.reshape(1, rows).to(out.dtype)                   # :894
+
+
 def triton_rvq_matmul_weight(stage_ids, codebooks, x_dtype):
     """The per-block weight of src/triton_id_matmul.py:195-208: the fp32 sum of
     all stages, cast to x.dtype.  stage_ids [S, N, B], codebooks [S, K, d]."""

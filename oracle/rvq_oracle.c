@@ -193,6 +193,36 @@ int or_reconstruct_weight_fast(const or_group* g, uint32_t active_mask,
   return 0;
 }
 
+int or_stagewise_linear(const or_group* g, const void* x, int x_dtype, int64_t m, void* y) {
+  if (check_group(g)) return -1;
+  if (g->block_scale) return -3;
+  const int64_t B = g->blocks_per_row, d = g->block_size, in = g->in_features;
+  for (int64_t i = 0; i < m; ++i) {
+    for (int64_t r = 0; r < g->rows; ++r) {
+      float out = 0.0f;
+      for (int s = 0; s < g->num_stages; ++s) {
+        const float ss = g->stage_scales ? or_round(or_load_f32(g->stage_scales, g->ss_dtype, s), x_dtype) : 1.0f;
+        double acc = 0.0;
+        for (int64_t b = 0; b < B; ++b) {
+          const int64_t id = load_id(g->stage_ids[s], g->id_dtype, r * B + b);
+          if (id < 0 || id >= g->codebook_size) return -2;
+          for (int64_t j = 0; j < d; ++j) {
+            const int64_t col = b * d + j;
+            if (col >= in) break;  /* zero padding of x (:883-885) */
+            float w = or_round(or_load_f32(g->codebooks[s], g->cb_dtype, id * d + j), x_dtype);
+            if (g->stage_scales) w = or_round(w * ss, x_dtype);
+            acc += (double)or_load_f32(x, x_dtype, i * in + col) * (double)w;
+          }
+        }
+        out = or_round(out + or_round((float)acc, x_dtype), x_dtype);
+      }
+      const float rs = or_round(or_load_f32(g->row_scale, g->rs_dtype, r / g->scale_rows), x_dtype);
+      store_out(y, x_dtype, i * g->rows + r, or_round(out * rs, x_dtype));
+    }
+  }
+  return 0;
+}
+
 void or_linear_f64(const void* x, int x_dtype, int64_t m, int64_t k,
                    const void* w, int w_dtype, int64_t n_rows,
                    const void* bias, int bias_dtype, double* y) {

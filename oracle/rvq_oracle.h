@@ -86,6 +86,16 @@ void or_triton_rvq_matmul(const void* x, int x_dtype, int64_t m, int64_t in_feat
                           int32_t block_size, const void* row_scale, int rs_dtype,
                           int out_dtype, void* out);
 
+/* stagewise_block_matmul (src/runtime.py:878-894), one group:
+ *   out = 0 (x dtype)                                                 :886
+ *   for every stage s: W_s = x_dtype(cb_s[id]) [* x_dtype(ss[s])]     :889-891
+ *                      out = x_dtype(out + x_dtype(x . W_s^T))         :892
+ *   y = x_dtype(out * x_dtype(row_scale))                              :894
+ * The per-stage dot is taken in double and rounded once to x dtype (torch's
+ * einsum accumulates in fp32 in an unspecified order).  x [m, in_features],
+ * y [m, rows] in x dtype bits.  Groups with block_scale are refused (-3). */
+int or_stagewise_linear(const or_group* g, const void* x, int x_dtype, int64_t m, void* y);
+
 /* Scalar route codebook, d = 1.
  * mode 0 = PackedIDRouteLinear.forward (src/runtime.py:89-97):
  *   W16 = f16(codebook_sum[id] * row_scale) then W16.to(x_dtype).

@@ -17,7 +17,7 @@ import zlib
 import pytest
 import torch
 
-from _cases import bits, make_encoding, module_buffers_as_encoding, oracle_weight, rel_err
+from _cases import bits, make_encoding, module_buffers_as_encoding, oracle_group, oracle_weight, rel_err
 from oracle import c_oracle
 from wal2026_amd import PackedGroupedBlockRVQLinear
 
@@ -138,6 +138,44 @@ def test_fast_strategy_parity(layout, m, gpu_device):
     else:
         w_ref = oracle_weight(module_buffers_as_encoding(mod), torch.bfloat16)
     assert rel_err(y, c_oracle.linear_f64(x, w_ref)) <= TOL
+
+
+STAGEWISE_LAYOUTS = [l for l in LAYOUTS if l[0] in {
+    "c1like_s2_u8", "s1_k4096_i16", "s1_k256_scale16_ragged_groups", "s3_groups256_ragged", "s4_u8",
+    "s2_stage_scales", "s2_bf16_codebooks", "d32_generic", "d4_padded_generic", "s5_generic"}]
+
+
+def _ulp_dist(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    def key(t):
+        v = bits(t).to(torch.int32) & 0xFFFF
+        return torch.where(v >= 0x8000, 0x8000 - v, v)
+    return (key(a) - key(b)).abs()
+
+
+@pytest.mark.parametrize("layout", STAGEWISE_LAYOUTS, ids=[l[0] for l in STAGEWISE_LAYOUTS])
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float16], ids=["xbf16", "xf16"])
+@pytest.mark.parametrize("m", [1, 33])
+def test_stagewise_strategy_parity(layout, x_dtype, m, gpu_device):
+    """stagewise_einsum (src/runtime.py:878-894, :1466-1475) against the
+    oracle.  The reference rounds every stage's contraction, every partial
+    sum and the bias add to x dtype, so two correct fp32-accumulating
+    implementations agree bit for bit except where accumulation order flips
+    one of those roundings: one x-dtype ulp of an intermediate, which
+    cancellation in the later adds can make a few ulps of a small output.
+    Bar: at least 98 % of outputs bit-equal, and max|dy| / max|y| within two
+    ulps of the largest output (2^-7 for bf16, 2^-9 for fp16)."""
+    mod = _module(layout, gpu_device, matmul_strategy="stagewise_einsum")
+    g = torch.Generator().manual_seed(7)
+    mod.bias = (torch.randn(mod.out_features, generator=g) * 0.1).to(torch.bfloat16).to(gpu_device)
+    x = torch.randn(m, mod.in_features, generator=g).to(x_dtype)
+    y = mod(x.to(gpu_device)).cpu()
+    assert y.dtype == x_dtype
+    enc = module_buffers_as_encoding(mod)
+    ref = torch.cat([c_oracle.stagewise_linear(oracle_group(ge), x) for ge in enc.groups], dim=1)
+    ref = (ref.float() + mod.bias.cpu().to(x_dtype).float()).to(x_dtype)
+    d = _ulp_dist(y, ref)
+    assert float((d == 0).double().mean()) >= 0.98, layout[0]
+    assert rel_err(y, ref) <= (2.0 ** -7 if x_dtype == torch.bfloat16 else 2.0 ** -9), layout[0]
 
 
 SCALED_LAYOUTS = [l for l in LAYOUTS if l[8].get("scale_run")]

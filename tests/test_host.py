@@ -76,10 +76,23 @@ def test_forward_on_cpu_fails_loudly():
 
 def test_unported_strategies_raise():
     enc = make_encoding(16, 32, S=1, seed=1)
-    for s, kw in [("stagewise_einsum", {}), ("full_weight_hot", {"hot_topk": 2})]:
-        mod = w.PackedGroupedBlockRVQLinear(enc, matmul_strategy=s, **kw)
-        with pytest.raises(NotImplementedError):
-            mod(torch.zeros(1, 32))
+    mod = w.PackedGroupedBlockRVQLinear(enc, matmul_strategy="full_weight_hot", hot_topk=2)
+    with pytest.raises(NotImplementedError):
+        mod(torch.zeros(1, 32))
+
+
+def test_stagewise_strategy_checks():
+    """stagewise_einsum runs on the GPU only, and refuses block-scaled groups
+    with the reference's ValueError (src/runtime.py:879-880)."""
+    mod = w.PackedGroupedBlockRVQLinear(make_encoding(16, 32, S=2, seed=1), matmul_strategy="stagewise_einsum")
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mod(torch.zeros(1, 32))
+    bs = w.PackedGroupedBlockRVQLinear(make_encoding(16, 32, S=2, block_scale=True, seed=1),
+                                       matmul_strategy="stagewise_einsum")
+    with pytest.raises(ValueError, match="unnormalized, transform-free"):
+        bs(torch.zeros(1, 32))
+    with pytest.raises(ValueError, match="unnormalized, transform-free"):
+        bs.groups[0].stagewise_block_matmul(torch.zeros(1, 32))
 
 
 def test_active_stage_indices_match_fixture():

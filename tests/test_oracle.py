@@ -233,3 +233,49 @@ def test_linearity_of_contraction():
     y12 = c_oracle.linear_f64(x1 + x2, w)
     assert torch.allclose(y12, c_oracle.linear_f64(x1, w) + c_oracle.linear_f64(x2, w), rtol=1e-5, atol=1e-6)
     assert not math.isnan(float(y12.sum()))
+
+
+def _ulp_dist(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Distance in units in the last place between two 16-bit float tensors
+    (monotone integer view of the bit patterns)."""
+    def key(t):
+        v = bits(t).to(torch.int32) & 0xFFFF
+        return torch.where(v >= 0x8000, 0x8000 - v, v)
+    return (key(a) - key(b)).abs()
+
+
+@pytest.mark.parametrize("x_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("S,stage_scales,in_f", [(1, False, 64), (2, True, 44), (3, False, 40)])
+def test_stagewise_matches_torch_ops(x_dtype, S, stage_scales, in_f):
+    """or_stagewise_linear against the reference's op sequence run by torch
+    (src/runtime.py:878-894).  Both round each stage's contraction to x dtype;
+    they may differ only where fp32 accumulation order flips that rounding, so
+    at most 1 ulp, and rarely."""
+    enc = make_encoding(24, in_f, d=8, S=S, K=64, stage_scales=stage_scales, seed=20 + S)
+    g0 = enc.groups[0]
+    x = torch.randn(5, in_f, generator=torch.Generator().manual_seed(3)).to(x_dtype)
+    got = c_oracle.stagewise_linear(oracle_group(g0), x)
+    want = ref_ops.stagewise_block_matmul(x, list(g0.stage_ids), list(g0.codebooks), g0.row_scale, in_f,
+                                          g0.stage_scales)
+    d = _ulp_dist(got, want)
+    assert int(d.max()) <= 1
+    assert float((d == 0).double().mean()) >= 0.95
+
+
+def test_stagewise_closed_form_single_stage():
+    """S = 1, unit row scale: y = round_x(x . round_x(cb[ids])^T), i.e. the
+    float64 contraction of the reconstructed weight rounded once."""
+    enc = make_encoding(16, 48, d=8, S=1, K=32, seed=31)
+    g0 = enc.groups[0]
+    g0 = type(g0)(**{**g0.__dict__, "row_scale": torch.ones_like(g0.row_scale)})
+    x = torch.randn(4, 48, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    got = c_oracle.stagewise_linear(oracle_group(g0), x)
+    w = c_oracle.reconstruct_weight(oracle_group(g0), torch.bfloat16)
+    want = c_oracle.linear_f64(x, w).float().to(torch.bfloat16)
+    assert torch.equal(bits(got), bits(want))
+
+
+def test_stagewise_rejects_block_scale():
+    enc = make_encoding(8, 16, d=8, S=1, K=16, block_scale=True, seed=2)
+    with pytest.raises(ValueError):
+        c_oracle.stagewise_linear(oracle_group(enc.groups[0]), torch.zeros(1, 16, dtype=torch.float16))

@@ -21,7 +21,7 @@ U8, I16, U16, I32 = 0, 1, 2, 3
 F16, BF16, F32 = 10, 11, 12
 
 # wal_rvq_semantics
-RECONSTRUCT, RECONSTRUCT_FAST = 0, 1
+RECONSTRUCT, RECONSTRUCT_FAST, STAGEWISE = 0, 1, 2
 
 # wal_status
 OK, EINVAL, EUNSUPPORTED, EHIP, ESIZE = 0, -1, -2, -3, -4

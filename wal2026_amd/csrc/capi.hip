@@ -188,6 +188,13 @@ int resolve_semantics(const wal_rvq_layer& L, int semantics, int* sem) {
     *sem = SEM_RECON;
     return WAL_OK;
   }
+  if (semantics == WAL_RVQ_STAGEWISE) {
+    // src/runtime.py:837-846, :879-880: block-scaled groups are refused
+    for (int g = 0; g < L.n_groups; ++g)
+      if (L.groups[g].block_scale) return fail(WAL_EUNSUPPORTED, "STAGEWISE on a group with block_scale");
+    *sem = SEM_STAGEWISE;
+    return WAL_OK;
+  }
   if (semantics != WAL_RVQ_RECONSTRUCT_FAST) return fail(WAL_EINVAL, "unknown semantics %d", semantics);
   int with_bs = 0;
   for (int g = 0; g < L.n_groups; ++g) with_bs += L.groups[g].block_scale != nullptr;
@@ -263,6 +270,7 @@ int image_args(const wal_rvq_layer* layer, int semantics, int x_dtype, int* sem)
   if (layer->block_size != 8) return fail(WAL_EUNSUPPORTED, "codebook images are for block_size 8 (got %d)", layer->block_size);
   if (layer->num_stages > 4) return fail(WAL_EUNSUPPORTED, "codebook images are for at most 4 stages");
   if (!is_half_dtype(x_dtype)) return fail(WAL_EINVAL, "x dtype must be F16 or BF16 (got %d)", x_dtype);
+  if (semantics == WAL_RVQ_STAGEWISE) return fail(WAL_EUNSUPPORTED, "STAGEWISE calls use no codebook image");
   return resolve_semantics(*layer, semantics, sem);
 }
 
@@ -302,6 +310,7 @@ int wal_rvq_reconstruct(const wal_rvq_layer* layer, int semantics, uint32_t acti
   if (!w_out) return fail(WAL_EINVAL, "w_out is NULL");
   if (!is_float_dtype(out_dtype)) return fail(WAL_EINVAL, "bad out dtype %d", out_dtype);
   int sem = 0;
+  if (semantics == WAL_RVQ_STAGEWISE) return fail(WAL_EINVAL, "STAGEWISE has no dense weight (it rounds per stage output)");
   if ((rc = resolve_semantics(*layer, semantics, &sem))) return rc;
   LayerArgs A = make_args(*layer, 0, resolve_mask(*layer, active_stage_mask));
   DtypeArgs D{layer->id_dtype, layer->codebook_dtype, layer->scale_dtype, out_dtype};
@@ -325,12 +334,17 @@ int wal_rvq_linear(const wal_rvq_layer* layer, int semantics, uint32_t active_st
   const uint32_t mask = resolve_mask(*layer, active_stage_mask);
   hipStream_t st = static_cast<hipStream_t>(stream);
   DtypeArgs D{layer->id_dtype, layer->codebook_dtype, layer->scale_dtype, x_dtype};
-  EpilogueArgs E{y, bias, (int64_t)layer->out_features, y_dtype, x_dtype, bias_dtype, bias ? 1 : 0};
+  // bias inside F.linear (mode 1), or added to the rounded stagewise output (mode 2, src/runtime.py:1470-1473)
+  EpilogueArgs E{y, bias, (int64_t)layer->out_features, y_dtype, x_dtype, bias_dtype,
+                 bias ? (sem == SEM_STAGEWISE ? 2 : 1) : 0};
   hipError_t e;
   if (layer->image != nullptr && layer->image_tag != WAL_RVQ_IMAGE_TAG(semantics, x_dtype))
     return fail(WAL_EINVAL, "the layer's codebook image was built for tag 0x%x, this call needs 0x%x",
                 layer->image_tag, WAL_RVQ_IMAGE_TAG(semantics, x_dtype));
-  if (m <= 16 && mfma_eligible(*layer, sem, x_dtype, x, false)) {
+  if (sem == SEM_STAGEWISE) {
+    LayerArgs A = make_args(*layer, 1, resolve_mask(*layer, 0));
+    e = launch_generic_linear(A, D, E, sem, x, m, st);
+  } else if (m <= 16 && mfma_eligible(*layer, sem, x_dtype, x, false)) {
     LayerArgs A = make_args(*layer, 0, mask);
     A.image = static_cast<const uint8_t*>(layer->image);
     e = launch_decode(A, D, E, sem, lds_mode_for(*layer, sem), x, (int)m, device_cu_count(), st);

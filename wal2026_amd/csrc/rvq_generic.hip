@@ -6,7 +6,7 @@
 //  * rvq_generic_linear_kernel: LDS-tiled fp32 VALU contraction with the weight
 //    tile dequantised element by element.  Handles what the MFMA kernels do not
 //    (any block size, 32-bit ids, fp32 codebooks, block_scale, unaligned rows)
-//    and the Triton / route-codebook semantics.
+//    and the Triton / route-codebook / stagewise semantics.
 #include "rvq_fragment.h"
 
 namespace wal {
@@ -73,6 +73,23 @@ WAL_DEVICE float weight_elem(const LayerArgs& L, const wal_rvq_group& g, const D
   }
 }
 
+// Stage s's contribution to W[r, col] under stagewise_block_matmul
+// (src/runtime.py:889-892): the codeword cast to x dtype, times the stage
+// scale cast to x dtype (product in x dtype).  No row scale: it is applied to
+// the contracted output.
+template <int DT>
+WAL_DEVICE float stage_elem(const LayerArgs& L, const wal_rvq_group& g, const DtypeArgs& D, int64_t r, int col,
+                            int s) {
+  const int d = L.block_size;
+  const int b = col / d;
+  const int j = col - b * d;
+  const int64_t slot = r * (int64_t)L.blocks_per_row + b;
+  const int64_t id = clamp_id(load_id(g.stage_ids[s], D.id_dtype, slot), L.codebook_size);
+  float c = round_dt<DT>(load_f(g.codebooks[s], D.cb_dtype, id * d + j));
+  if (g.stage_scales) c = round_dt<DT>(c * round_dt<DT>(load_f(g.stage_scales, D.sc_dtype, s)));
+  return c;
+}
+
 template <int DT>
 WAL_DEVICE void store_elem(void* out, int64_t i, float v) {
   if constexpr (DT == WAL_F32) reinterpret_cast<float*>(out)[i] = v;
@@ -125,7 +142,18 @@ __global__ __launch_bounds__(256) void rvq_generic_linear_kernel(LayerArgs L, Dt
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
   constexpr int XDT = (DT == WAL_F32) ? WAL_F32 : DT;
+  // SEM_STAGEWISE makes one pass per stage: out = round_x(out + round_x(x . W_s))
+  // from out = +0 (src/runtime.py:886-893); every other semantics one pass.
+  const int n_pass = SEM == SEM_STAGEWISE ? L.num_stages : 1;
+  float out_sw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out_sw[i] = 0.0f;
 
+  for (int pass = 0; pass < n_pass; ++pass) {
+  if (SEM == SEM_STAGEWISE) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  }
   for (int k0 = 0; k0 < L.in_features; k0 += GK) {
     // weight tile: 64 x 32 elements, 8 per thread
     for (int e = tid; e < GN * GK; e += 256) {
@@ -134,12 +162,16 @@ __global__ __launch_bounds__(256) void rvq_generic_linear_kernel(LayerArgs L, Dt
       float w = 0.0f;
       if (rr < ti.rows && col < L.in_features) {
         const int64_t r = ti.row0 + rr;
-        float rs = 1.0f;
-        if (SEM != SEM_TRITON) {
-          const int64_t rsi = (SEM == SEM_ROUTE0 || SEM == SEM_ROUTE1) ? r : scale_index(L, r);
-          rs = load_f(g.row_scale, D.sc_dtype, rsi);
+        if constexpr (SEM == SEM_STAGEWISE) {
+          w = stage_elem<DT>(L, g, D, r, col, pass);
+        } else {
+          float rs = 1.0f;
+          if (SEM != SEM_TRITON) {
+            const int64_t rsi = (SEM == SEM_ROUTE0 || SEM == SEM_ROUTE1) ? r : scale_index(L, r);
+            rs = load_f(g.row_scale, D.sc_dtype, rsi);
+          }
+          w = weight_elem<SEM, DT>(L, g, D, r, col, rs);
         }
-        w = weight_elem<SEM, DT>(L, g, D, r, col, rs);
       }
       ws[rr][kk] = w;
     }
@@ -158,16 +190,24 @@ __global__ __launch_bounds__(256) void rvq_generic_linear_kernel(LayerArgs L, Dt
     }
     __syncthreads();
   }
+  if (SEM == SEM_STAGEWISE) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out_sw[i] = round_dt<DT>(out_sw[i] + round_dt<DT>(acc[i]));
+  }
+  }  // pass
   (void)XDT;
   if (tn >= ti.rows) return;
   const int64_t n = ti.out_row0 + tn;
   float rho = 1.0f;
   if (SEM == SEM_TRITON) rho = load_f(g.row_scale, D.sc_dtype, ti.row0 + tn);
+  // stagewise: out * row_scale.to(out.dtype), product in x dtype (src/runtime.py:894)
+  if (SEM == SEM_STAGEWISE) rho = round_dt<DT>(load_f(g.row_scale, D.sc_dtype, scale_index(L, ti.row0 + tn)));
   for (int i = 0; i < 8; ++i) {
     const int64_t m = m0 + tm * 8 + i;
     if (m >= M) break;
     float v = acc[i];
     if (SEM == SEM_TRITON) v = v * rho;  // src/triton_id_matmul.py:210
+    if (SEM == SEM_STAGEWISE) v = round_dt<DT>(out_sw[i] * rho);
     store_output(E, m, n, v);
   }
 }
@@ -217,6 +257,7 @@ hipError_t launch_generic_linear(const LayerArgs& L, const DtypeArgs& D, const E
     case SEM_TRITON: return generic_dt<SEM_TRITON>(L, D, E, x, M, st);
     case SEM_ROUTE0: return generic_dt<SEM_ROUTE0>(L, D, E, x, M, st);
     case SEM_ROUTE1: return generic_dt<SEM_ROUTE1>(L, D, E, x, M, st);
+    case SEM_STAGEWISE: return generic_dt<SEM_STAGEWISE>(L, D, E, x, M, st);
     default: return generic_dt<SEM_RECON>(L, D, E, x, M, st);
   }
 }

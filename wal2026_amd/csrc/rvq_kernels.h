@@ -11,7 +11,8 @@ enum Semantics : int {
   SEM_FAST = 1,    // reconstruct_weight_fast, src/runtime.py:568-598
   SEM_TRITON = 2,  // _rvq_group_linear_kernel, src/triton_id_matmul.py:186-216
   SEM_ROUTE0 = 3,  // PackedIDRouteLinear.forward, src/runtime.py:89-97
-  SEM_ROUTE1 = 4   // _id_route_linear_kernel, src/triton_id_matmul.py:55-62
+  SEM_ROUTE1 = 4,  // _id_route_linear_kernel, src/triton_id_matmul.py:55-62
+  SEM_STAGEWISE = 5  // stagewise_block_matmul, src/runtime.py:878-894
 };
 
 struct DtypeArgs {

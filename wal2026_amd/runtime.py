@@ -16,8 +16,10 @@ Strategy mapping for ``PackedGroupedBlockRVQLinear`` (src/runtime.py:1362-1507):
   over the active stages (src/runtime.py:568-598).
 * ``triton_block_rvq``: per group, the fused Triton kernel's arithmetic where
   the reference would run it (src/runtime.py:1476-1489), else reconstruct_weight.
-* ``stagewise_einsum`` and the experimental hot/cold / palette strategies are
-  accepted by the constructor (same validation as the reference) but raise
+* ``stagewise_einsum``: stagewise_block_matmul's per-stage rounding
+  (src/runtime.py:878-894), one launch for all row groups.
+* The experimental hot/cold / palette strategies are accepted by the
+  constructor (same validation as the reference) but raise
   NotImplementedError in forward.
 """
 from __future__ import annotations
@@ -388,8 +390,29 @@ class PackedBlockRVQGroup(nn.Module):
         return rvq_group_linear_matmul(x_flat, stage_ids, codebooks, self.row_scale)
 
     def stagewise_block_matmul(self, x_flat: Tensor) -> Tensor:
-        raise NotImplementedError("wal2026_amd: stagewise_einsum (src/runtime.py:878-894) is not implemented; "
-                                  "use matmul_strategy='hip_block_rvq'")
+        """src/runtime.py:878-894 on the GPU: per stage, the codewords in x
+        dtype contracted and rounded to x dtype, summed in x dtype over all
+        stages, times row_scale in x dtype."""
+        if not self.supports_stagewise_block_matmul():
+            raise ValueError("stagewise_block_matmul only supports unnormalized, transform-free encodings")
+        return _stagewise_linear(self._descriptor(), x_flat, self.out_features, None)
+
+
+def _stagewise_linear(desc: _LayerDesc, x_flat: Tensor, out_features: int, bias: Tensor | None,
+                      out_dtype: torch.dtype | None = None) -> Tensor:
+    """One STAGEWISE launch over every group of ``desc``; the bias (the
+    module's bf16 buffer) is cast to x dtype and added to the rounded result
+    (src/runtime.py:1466-1475)."""
+    dev = _lib.require_rocm(x_flat)
+    x_c = x_flat.contiguous()
+    y = torch.empty(x_c.shape[0], out_features, dtype=out_dtype or x_flat.dtype, device=dev)
+    if x_c.shape[0] == 0:
+        return y
+    btag = _lib.float_tag(bias.dtype) if bias is not None else _lib.F32
+    _lib.check(_lib.lib().wal_rvq_linear(ctypes.byref(desc.layer), _lib.STAGEWISE, 0, x_c.data_ptr(), x_c.shape[0],
+                                         _lib.float_tag(x_c.dtype), _ptr(bias), btag, y.data_ptr(),
+                                         _lib.float_tag(y.dtype), _lib.stream_ptr(dev)))
+    return y
 
 
 class PackedGroupedBlockRVQLinear(nn.Module):
@@ -528,6 +551,14 @@ class PackedGroupedBlockRVQLinear(nn.Module):
                                       _lib.float_tag(y.dtype), stream))
         return y
 
+    def _stagewise(self, x_flat: Tensor, out_dtype: torch.dtype | None = None) -> Tensor:
+        """Strategy stagewise_einsum (src/runtime.py:1466-1475): every group's
+        stagewise_block_matmul plus its bias slice, in one launch."""
+        for g in self.groups:
+            if not g.supports_stagewise_block_matmul():
+                raise ValueError("stagewise_block_matmul only supports unnormalized, transform-free encodings")
+        return _stagewise_linear(self._descriptor(), x_flat, self.out_features, self.bias, out_dtype)
+
     def _triton_strategy(self, x_flat: Tensor) -> Tensor:
         """src/runtime.py:1476-1489: fused-kernel arithmetic on the groups the
         reference would run it on, reconstruct_weight + linear elsewhere; the
@@ -554,8 +585,7 @@ class PackedGroupedBlockRVQLinear(nn.Module):
         elif s == "triton_block_rvq":
             out = self._triton_strategy(x_flat)
         elif s == "stagewise_einsum":
-            raise NotImplementedError("wal2026_amd: stagewise_einsum (src/runtime.py:878-894) is not implemented; "
-                                      "use matmul_strategy='hip_block_rvq'")
+            out = self._stagewise(x_flat)
         else:
             raise NotImplementedError(f"wal2026_amd: matmul_strategy={s!r} is one of the reference's experimental "
                                       "hot/cold or palette strategies, which this runtime does not implement; use "
