@@ -17,6 +17,11 @@ measured live with HIP events, CPU baseline of the reference's per_group op
 sequence timed on this host's cores).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--m 1]
+
+With --config c4 (M = 2048, two-stage 256-entry codebooks, uint8 indices) the
+same stack runs the prefill kernel instead and the roofline is the bf16 MFMA
+one: algorithmic flops (2 M N K per linear) of the dominant launch over its
+measured duration, against the 2.5 PFLOP/s dense peak.
 """
 from __future__ import annotations
 
@@ -150,15 +155,16 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c5"])
-    ap.add_argument("--m", type=int, default=1)
+    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--m", type=int, default=None, help="activation rows (default: the config's, 1 for c3)")
     ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run the dominant launch N times per layer, then one 256 MiB device copy "
                          "(the calibration kernel); for rocprofv3 --pmc runs")
-    ap.add_argument("--pmc-summary", default=str(ROOT / "profiles" / "decode_c3_gate_up_pmc.txt"),
-                    help="rocprofv3 --pmc summary giving the dominant kernel's HBM traffic (optional)")
+    ap.add_argument("--pmc-summary", default=None,
+                    help="rocprofv3 --pmc summary giving the dominant kernel's HBM traffic (default: "
+                         "profiles/<decode|prefill>_<config>_<launch>_pmc.txt when it exists)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (the path has no multi-GPU code); "
@@ -169,7 +175,7 @@ def main() -> int:
         return 1
 
     cfg = synth.CONFIGS[args.config]
-    if args.m != cfg.m:
+    if args.m is not None and args.m != cfg.m:
         cfg = synth.Config(**{**cfg.__dict__, "m": args.m})
     layers = args.layers or cfg.layers
     dev = torch.device("cuda", 0)
@@ -263,6 +269,36 @@ def main() -> int:
         us = time_kernel_family([layer[name] for layer in stack], xs[k], reps=1)
         per_linear[name] = {"us": round(us, 3), "GBps": round(linear_bytes(cfg, n, k) / (us * 1e-6) / 1e9, 1)}
     layer_bytes = cfg.compressed_bytes_per_layer()
+    prefill = cfg.m > 16
+    kind = "prefill" if prefill else "decode"
+    pmc_summary = args.pmc_summary or str(ROOT / "profiles" / f"{kind}_{cfg.name}_{dom_name}_pmc.txt")
+    if prefill:
+        dom_flops = sum(2 * cfg.m * shape[m_][0] * shape[m_][1] for f, members in fuse if f == dom_name
+                        for m_ in members) or 2 * cfg.m * shape[dom_name][0] * shape[dom_name][1]
+        tflops = dom_flops / (dom_us * 1e-6) / 1e12
+        roofline = {
+            "bound": "mfma",
+            "kernel": f"rvq_prefill_kernel ({dom_name}, {dom_flops} flop)",
+            "achieved": round(tflops, 1),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "avg_launch_us": round(dom_us, 3),
+            "algorithmic_flops_per_launch": dom_flops,
+            "traffic": traffic_bytes(pmc_summary),
+        }
+    else:
+        roofline = {
+            "bound": "hbm",
+            "kernel": f"rvq_decode_kernel ({dom_name}, {dom_bytes} compressed bytes)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "avg_launch_us": round(dom_us, 3),
+            "algorithmic_bytes_per_launch": dom_bytes,
+            "traffic": traffic_bytes(pmc_summary),
+        }
 
     result = {
         "metric": "RVQ-GEMV us/layer & %HBM roofline (M=1); decode tok/s at Llama-8B shapes",
@@ -281,7 +317,7 @@ def main() -> int:
             "workload": f"{cfg.name}: Llama-3-8B-shaped {layers}-layer stack of compressed linears, "
                         f"S={cfg.num_stages}, K={cfg.codebook_size}, d={cfg.block_size}, "
                         f"{str(cfg.ids_dtype()).replace('torch.', '')} ids, scale per {cfg.scale_rows} rows, "
-                        f"decode M={cfg.m}, one HIP graph per step; linears sharing an input fused "
+                        f"{kind} M={cfg.m}, one HIP graph per step; linears sharing an input fused "
                         f"({', '.join(f for f, _ in fuse)})",
             "layers": layers,
             "m": cfg.m,
@@ -293,18 +329,10 @@ def main() -> int:
             "per_launch": per_launch,
             "per_linear_unfused": per_linear,
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": f"rvq_decode_kernel ({dom_name}, {dom_bytes} compressed bytes)",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "avg_launch_us": round(dom_us, 3),
-            "algorithmic_bytes_per_launch": dom_bytes,
-            "traffic": traffic_bytes(args.pmc_summary),
-        },
+        "roofline": roofline,
     }
+    if prefill:
+        result["config"]["tflops_per_step"] = round(cfg.flops_per_layer() * layers / (ms_per_step * 1e-3) / 1e12, 1)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(cfg)

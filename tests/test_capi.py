@@ -72,10 +72,10 @@ def test_plan_tables():
     toff = struct.unpack_from("<3i", raw, 16)
     ntiles = struct.unpack_from("<3i", raw, 28)
     assert magic == 0x57524C31 and n_groups == 3
-    # tile kinds of 16, 64 and 128 rows; tiles never straddle groups
-    assert ntiles == (16 + 16 + 7, 4 + 4 + 2, 2 + 2 + 1)
-    t128 = [struct.unpack_from("<4i", raw, toff[2] + 16 * i) for i in range(ntiles[2])]
-    assert t128 == [(0, 0, 128, 0), (0, 128, 128, 128), (1, 0, 128, 256), (1, 128, 128, 384), (2, 0, 100, 512)]
+    # tile kinds of 16, 64 and 256 rows; tiles never straddle groups
+    assert ntiles == (16 + 16 + 7, 4 + 4 + 2, 1 + 1 + 1)
+    t256 = [struct.unpack_from("<4i", raw, toff[2] + 16 * i) for i in range(ntiles[2])]
+    assert t256 == [(0, 0, 256, 0), (1, 0, 256, 256), (2, 0, 100, 512)]
     t16 = [struct.unpack_from("<4i", raw, toff[0] + 16 * i) for i in range(ntiles[0])]
     assert t16[-1] == (2, 96, 4, 608)
     # the group table is a verbatim copy of the host array

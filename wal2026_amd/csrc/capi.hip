@@ -176,9 +176,10 @@ bool mfma_eligible(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, 
     if ((int64_t)L.groups[g].rows * L.blocks_per_row * id_bytes(L.id_dtype) >= (int64_t)1 << 31) return false;
   const int esz = lds_mode_for(L, sem) == LM_F32 ? 32 : 16;
   const size_t cb = (size_t)L.num_stages * L.codebook_size * esz;
-  // prefill: four 128 x 72 16-bit tiles; decode: the partial sums of one
-  // tile from 8 waves at M = 16 and the zero row
-  const size_t budget = prefill ? (160 * 1024 - 4 * 128 * 72 * 2) : (160 * 1024 - 8 * 1024 - 256);
+  // prefill: double-buffered 128 x 40 and 256 x 40 16-bit tiles (the short
+  // x tile); decode: the partial sums of one tile from 8 waves at M = 16 and
+  // the zero row
+  const size_t budget = prefill ? (160 * 1024 - 2 * (128 + 256) * 40 * 2) : (160 * 1024 - 8 * 1024 - 256);
   return cb <= budget;
 }
 
@@ -350,7 +351,7 @@ int wal_rvq_linear(const wal_rvq_layer* layer, int semantics, uint32_t active_st
     e = launch_decode(A, D, E, sem, lds_mode_for(*layer, sem), x, (int)m, device_cu_count(), st);
   } else if (m > 16 && mfma_eligible(*layer, sem, x_dtype, x, true)) {
     LayerArgs A = make_args(*layer, 2, mask);
-    e = launch_prefill(A, D, E, sem, lds_mode_for(*layer, sem), x, m, st);
+    e = launch_prefill(A, D, E, sem, lds_mode_for(*layer, sem), x, m, device_cu_count(), st);
   } else {
     LayerArgs A = make_args(*layer, 1, mask);
     e = launch_generic_linear(A, D, E, sem, x, m, st);

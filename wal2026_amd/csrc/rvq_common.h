@@ -69,7 +69,7 @@ WAL_DEVICE T ldg(const void* p, int64_t i) { return ((const __attribute__((addre
 // ---------------------------------------------------------------------------
 constexpr int kPlanMagic = 0x57524c31;  // "WRL1"
 constexpr int kNumTileKinds = 3;
-constexpr int kTileRows[kNumTileKinds] = {16, 64, 128};
+constexpr int kTileRows[kNumTileKinds] = {16, 64, 256};
 
 struct PlanTile {
   int32_t group;

@@ -72,7 +72,7 @@ hipError_t decode_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueAr
                         const void* x, int M, int n_cu, hipStream_t st);
 template <int XDT, typename IdT>
 hipError_t prefill_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                         const void* x, int64_t M, hipStream_t st);
+                         const void* x, int64_t M, int n_cu, hipStream_t st);
 
 // One explicit instantiation per (activation dtype, index width), each in its
 // own translation unit (rvq_decode_<x>_<ids>.hip, rvq_prefill_<x>_<ids>.hip);
@@ -86,13 +86,13 @@ extern template hipError_t decode_entry<WAL_F16, uint8_t>(const LayerArgs&, cons
 extern template hipError_t decode_entry<WAL_F16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
                                                            int, int, const void*, int, int, hipStream_t);
 extern template hipError_t prefill_entry<WAL_BF16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                            int, int, const void*, int64_t, hipStream_t);
+                                                            int, int, const void*, int64_t, int, hipStream_t);
 extern template hipError_t prefill_entry<WAL_BF16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                             int, int, const void*, int64_t, hipStream_t);
+                                                             int, int, const void*, int64_t, int, hipStream_t);
 extern template hipError_t prefill_entry<WAL_F16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                           int, int, const void*, int64_t, hipStream_t);
+                                                           int, int, const void*, int64_t, int, hipStream_t);
 extern template hipError_t prefill_entry<WAL_F16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                            int, int, const void*, int64_t, hipStream_t);
+                                                            int, int, const void*, int64_t, int, hipStream_t);
 
 inline hipError_t launch_decode(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
                                 int lds_mode, const void* x, int M, int n_cu, hipStream_t st) {
@@ -106,14 +106,14 @@ inline hipError_t launch_decode(const LayerArgs& L, const DtypeArgs& D, const Ep
 }
 
 inline hipError_t launch_prefill(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
-                                 int lds_mode, const void* x, int64_t M, hipStream_t st) {
+                                 int lds_mode, const void* x, int64_t M, int n_cu, hipStream_t st) {
   if (L.n_tiles == 0 || M == 0) return hipSuccess;
   const bool wide = D.id_dtype != WAL_U8;
   if (D.x_dtype == WAL_BF16)
-    return wide ? prefill_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, st)
-                : prefill_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, st);
-  return wide ? prefill_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, st)
-              : prefill_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, st);
+    return wide ? prefill_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, n_cu, st)
+                : prefill_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, n_cu, st);
+  return wide ? prefill_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, n_cu, st)
+              : prefill_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, n_cu, st);
 }
 
 }  // namespace wal
