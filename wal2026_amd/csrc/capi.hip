@@ -175,11 +175,12 @@ bool mfma_eligible(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, 
   for (int g = 0; g < L.n_groups; ++g)
     if ((int64_t)L.groups[g].rows * L.blocks_per_row * id_bytes(L.id_dtype) >= (int64_t)1 << 31) return false;
   const int esz = lds_mode_for(L, sem) == LM_F32 ? 32 : 16;
-  const size_t cb = (size_t)L.num_stages * L.codebook_size * esz;
-  // prefill: double-buffered 128 x 40 and 256 x 40 16-bit tiles (the short
-  // x tile); decode: the partial sums of one tile from 8 waves at M = 16 and
-  // the zero row
-  const size_t budget = prefill ? (160 * 1024 - 2 * (128 + 256) * 40 * 2) : (160 * 1024 - 8 * 1024 - 256);
+  // (prefill: 8-bit ids with K < 256 get a 256-entry margin, see rvq_prefill_impl.h)
+  const size_t cb = ((size_t)L.num_stages * L.codebook_size +
+                     (prefill && L.id_dtype == WAL_U8 && L.codebook_size < 256 ? 256 - L.codebook_size : 0)) * esz;
+  // prefill: double-buffered 128 x 48 and 256 x 48 16-bit tiles; decode: the
+  // partial sums of one tile from 8 waves at M = 16 and the zero row
+  const size_t budget = prefill ? (160 * 1024 - 2 * (128 + 256) * 48 * 2) : (160 * 1024 - 8 * 1024 - 256);
   return cb <= budget;
 }
 

@@ -59,6 +59,10 @@ WAL_DEVICE u32x4_t ldbuf128_stream(bufrsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
 }
 WAL_DEVICE uint32_t ldbuf16(bufrsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
+// 16 bytes at byte offset off, cached (data other workgroups read again).
+WAL_DEVICE u32x4_t ldbuf128(bufrsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
 
 // Scalar element of a global buffer.
 template <typename T>

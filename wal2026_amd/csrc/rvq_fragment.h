@@ -331,18 +331,52 @@ WAL_DEVICE void stage_codebooks(uint8_t* lds, const GroupPtrs<S>& g, int K, cons
 // 8-weight fragment for stage ids id[0..S-1]: the pre-scale values in x
 // dtype (RECON: rne_x of the fp32 stage sum; FAST: the x-dtype stage sum),
 // then the row-scale product.
+// The LDS entries of one block's S codewords (gather_wfrag), and the 8
+// weights made from them (combine_wfrag); split so that a caller can issue the
+// gathers of several blocks before it waits for the first.
+template <int S, int LMODE>
+struct WfragRaw {
+  u32x4_t c[S][LMODE == LM_F32 ? 2 : 1];
+};
+
+template <int S, int LMODE>
+WAL_DEVICE WfragRaw<S, LMODE> gather_wfrag(const uint8_t* lds, const uint32_t (&id)[S], int K) {
+  WfragRaw<S, LMODE> r;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if constexpr (LMODE == LM_F32) {
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(lds + ((size_t)s * K + id[s]) * 32);
+      r.c[s][0] = p[0];
+      r.c[s][1] = p[1];
+    } else {
+      r.c[s][0] = *reinterpret_cast<const u32x4_t*>(lds + ((size_t)s * K + id[s]) * 16);
+    }
+  }
+  return r;
+}
+
+// gather_wfrag from a table replicated 1 << rshift times entry by entry
+// (entry e, copy c at ((e << rshift) + c) * ESZ); lds_lane already points at
+// this lane's copy.  Lanes that read in the same LDS cycle use different
+// copies, which sit in different banks, so random codewords do not conflict.
+template <int S, int LMODE>
+WAL_DEVICE WfragRaw<S, LMODE> gather_wfrag_rep(const uint8_t* lds_lane, const uint32_t (&id)[S], int K, int rshift) {
+  constexpr int ESZ = LMODE == LM_F32 ? 32 : 16;
+  WfragRaw<S, LMODE> r;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const uint8_t* p = lds_lane + ((uint32_t)((s * K + (int)id[s]) * ESZ) << rshift);
+    r.c[s][0] = *reinterpret_cast<const u32x4_t*>(p);
+    if constexpr (LMODE == LM_F32) r.c[s][1] = *reinterpret_cast<const u32x4_t*>(p + 16);
+  }
+  return r;
+}
+
 template <int S, int LMODE, int SEM, int XDT>
-WAL_DEVICE u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S], int K, uint32_t active,
-                              const RowScale& rs) {
+WAL_DEVICE u32x4_t combine_wfrag(const WfragRaw<S, LMODE>& raw, uint32_t active, const RowScale& rs) {
   u32x4_t a;
   if constexpr (LMODE == LM_F32) {
-    u32x4_t c[S][2];
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(lds + ((size_t)s * K + id[s]) * 32);
-      c[s][0] = p[0];
-      c[s][1] = p[1];
-    }
+    const auto& c = raw.c;
 #pragma unroll
     for (int pr = 0; pr < 4; ++pr) {
       const int h = pr >> 1, o = (pr & 1) * 2;
@@ -358,7 +392,7 @@ WAL_DEVICE u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S], int K
   } else {
     u32x4_t c[S];
 #pragma unroll
-    for (int s = 0; s < S; ++s) c[s] = *reinterpret_cast<const u32x4_t*>(lds + ((size_t)s * K + id[s]) * 16);
+    for (int s = 0; s < S; ++s) c[s] = raw.c[s][0];
     if constexpr (LMODE == LM_H16) {
       // stage 0 is staged as 0 + v, so c0 + c1 + ... equals the reference's
       // ((0 + c0) + c1) + ... bit for bit, signed zeros included
@@ -397,6 +431,14 @@ WAL_DEVICE u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S], int K
     }
   }
   return scale_frag<XDT>(a, rs);
+}
+
+// The 8 weights of one block: gather the S codewords from the staged table,
+// rebuild the reference's dequantised values, apply the row scale.
+template <int S, int LMODE, int SEM, int XDT>
+WAL_DEVICE u32x4_t make_wfrag(const uint8_t* lds, const uint32_t (&id)[S], int K, uint32_t active,
+                              const RowScale& rs) {
+  return combine_wfrag<S, LMODE, SEM, XDT>(gather_wfrag<S, LMODE>(lds, id, K), active, rs);
 }
 
 template <int XDT>

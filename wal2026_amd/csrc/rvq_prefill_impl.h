@@ -5,15 +5,30 @@
 // arrangement; a wave owns 16 TM x 64 outputs = TM x 4 tiles of
 // v_mfma_f32_16x16x32_{bf16,f16}.  Per k-step every thread
 //   * dequantises 2 blocks (16 weights) of one weight row from the LDS
-//     codebooks with the reference's exact rounding (make_wfrag) into the W
-//     tile in LDS, in the MFMA input dtype, and
+//     codebooks with the reference's exact rounding (rvq_fragment.h) into the
+//     W tile in LDS, in the MFMA input dtype, and
 //   * copies one or two 16-byte pieces of x (the tile is BM rows x 64 bytes)
 //     into the x tile in LDS.
-// Both tiles are double-buffered.  The x pieces are loaded two k-steps ahead
-// and the index bytes (16 blocks = 4 k-steps per load) one load group ahead,
-// so the loads have two MFMA phases to arrive.  Rows are padded by 16 bytes
-// (80-byte stride) so the 16 rows a ds_read_b128 fragment read touches fall in
-// distinct banks.
+// Pipeline (iteration k): the MFMAs of step k run on operand fragments
+// already in registers while the fragments of step k + 1 are read from LDS
+// buffer (k + 1) & 1 and step k + 2 is dequantised into buffer k & 1, whose
+// fragments every wave read before the previous barrier; one barrier per
+// step.  x is loaded four steps ahead, index bytes (16 blocks = 4 steps per
+// load) a group ahead.  Loads are unconditional buffer loads (out-of-range
+// offsets read zeros), so a step is one basic block and the compiler's load
+// counters stay exact.
+//
+// LDS rows are 96 bytes apart: a 16 x 16 fragment read (lane l: row l % 16,
+// 16-byte chunk l / 16) is then conflict-free on gfx950's 64-bank LDS, which
+// serves lanes 0-7 with 16-23 (and so on) in one cycle; an 80-byte stride
+// measures 2-way conflicted.  The codebook table is replicated (as many
+// copies as LDS holds, up to 8) so lanes gathering in the same cycle mostly
+// hit different copies.
+//
+// Measured on gfx950: the dequantisation arithmetic does not overlap the
+// MFMAs of the same SIMD (their costs add), so the kernel's rate is set by
+// the VALU work per weight (about four full-rate instructions per element)
+// amortised over the BM rows that use it.
 //
 // Grid: the x-row tile index varies fastest, so consecutive workgroups (which
 // the dispatcher deals round-robin to the XCDs) share one weight tile and each
@@ -27,20 +42,38 @@ namespace wal {
 constexpr int kPrefillThreads = 512;
 constexpr int PBN = 256;        // weight rows per workgroup tile
 constexpr int PBK = 32;         // k per step
-constexpr int PSTR = PBK + 8;   // elements per LDS row (80 bytes)
+constexpr int PSTR = PBK + 16;  // elements per LDS row (96 bytes; see below)
 
 template <int TM>
 constexpr int prefill_bm() { return 32 * TM; }
 
-template <int S, int LMODE>
-WAL_HOST_DEVICE size_t prefill_lds_bytes(int TM, int K) {
-  return (size_t)2 * (32 * TM + PBN) * PSTR * sizeof(uint16_t) + (size_t)S * K * lds_entry_bytes<LMODE>();
+// Staged table entries: S tables of K entries back to back, plus, for 8-bit
+// indices and K < 256, the 256 - K entries that keep any index byte of the
+// last stage inside the allocation (8-bit ids are not clamped).
+template <int S, typename IdT>
+WAL_HOST_DEVICE int prefill_table_entries(int K) {
+  return S * K + ((sizeof(IdT) == 1 && K < 256) ? 256 - K : 0);
 }
+
+template <int TM>
+WAL_HOST_DEVICE size_t prefill_tile_bytes() {
+  return (size_t)2 * (32 * TM + PBN) * PSTR * sizeof(uint16_t);
+}
+
+// LDS of a launch whose codebook table is replicated 1 << rshift times.
+template <int S, typename IdT, int LMODE>
+WAL_HOST_DEVICE size_t prefill_lds_bytes(int TM, int K, int rshift) {
+  return (TM == 8 ? prefill_tile_bytes<8>() : prefill_tile_bytes<4>()) +
+         ((size_t)prefill_table_entries<S, IdT>(K) * lds_entry_bytes<LMODE>() << rshift);
+}
+
+// sched_group_barrier masks
+constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgDsRead = 0x100, kSgDsWrite = 0x200, kSgVmemRead = 0x020;
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int TM>
 __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
                                                                       const uint16_t* __restrict__ x, int64_t M,
-                                                                      int n_mt) {
+                                                                      int n_mt, int rshift) {
   constexpr int BM = prefill_bm<TM>();
   constexpr int XP = BM * 4 / kPrefillThreads;  // 16-byte x pieces per thread per k-step (1 or 2)
   constexpr int NV = sizeof(IdT);                // 16-byte index loads per stage per group of 4 k-steps
@@ -65,40 +98,67 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
   const int nk = B / 4;  // B % 16 == 0 (host contract): whole k-steps, whole index groups
   const uint32_t kmax = (uint32_t)(K - 1);
 
-  stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, ti.p, K, D);
+  // Codebook table, replicated 1 << rshift times (host choice: as many
+  // copies, up to 8, as LDS holds): staged compactly into the idle W tile
+  // area, then spread into the replicated layout.
+  constexpr int ESZ = lds_entry_bytes<LMODE>();
+  if (rshift == 0) {
+    stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, ti.p, K, D);
+  } else {
+    uint8_t* compact = reinterpret_cast<uint8_t*>(ws);
+    stage_codebooks<S, LMODE, SEM, XDT>(compact, ti.p, K, D);
+    __syncthreads();
+    const int n16 = prefill_table_entries<S, IdT>(K) * (ESZ / 16);  // 16-byte pieces
+    const int nc = 1 << rshift;
+    for (int i = tid; i < n16 * nc; i += kPrefillThreads) {
+      const int piece = i >> rshift, c = i & (nc - 1);
+      const int e = piece / (ESZ / 16), h = piece - e * (ESZ / 16);
+      *reinterpret_cast<u32x4_t*>(lds_cb + (((e << rshift) + c) * ESZ) + 16 * h) =
+          *reinterpret_cast<const u32x4_t*>(compact + (size_t)piece * 16);
+    }
+  }
+  const uint8_t* lds_lane = lds_cb + (lane & ((1 << rshift) - 1)) * ESZ;  // this lane's copy
 
-  // dequantiser role: weight row wr_l, blocks 2 * wh + {0, 1} of every k-step
+  // dequantiser role: weight row wr_l, blocks 2 * wh + {0, 1} of every k-step.
+  // Rows past the tile dequantise the tile's first row; their outputs are
+  // never stored.
   const int wr_l = tid >> 1, wh = tid & 1;
-  const bool w_row_ok = wr_l < ti.rows;
-  const int64_t wr = ti.row0 + (w_row_ok ? wr_l : 0);
-  const float rs_raw = w_row_ok ? load_f(ti.p.row_scale, D.sc_dtype, scale_index(L, wr)) : 0.0f;
-  const RowScale rs = make_row_scale<XDT>(rs_raw);
-  const IdT* idp[S];
+  const int64_t wr = ti.row0 + (wr_l < ti.rows ? wr_l : 0);
+  const RowScale rs = make_row_scale<XDT>(load_f(ti.p.row_scale, D.sc_dtype, scale_index(L, wr)));
+  // index planes: one descriptor per stage on the group's base (uniform; a
+  // per-lane base would make the compiler loop over the lanes' descriptors),
+  // the row in the per-lane offset (rows * B * sizeof(IdT) < 2^31, host check)
+  bufrsrc_t idr[S];
 #pragma unroll
-  for (int s = 0; s < S; ++s) idp[s] = reinterpret_cast<const IdT*>(ti.p.ids[s]) + wr * B;
+  for (int s = 0; s < S; ++s) idr[s] = make_rsrc(ti.p.ids[s]);
+  const uint32_t idrow = (uint32_t)(wr * B * (int64_t)sizeof(IdT));
 
-  // x loader role: piece p = tid + i * 512 -> row p / 4, 16-byte column p % 4
-  const uint16_t* xrow[XP];
-  bool xok[XP];
+  // x loader role: piece p = tid + i * 512 -> row p / 4, 16-byte column p % 4,
+  // addressed from the tile's first row (rows past M read zeros)
+  const bufrsrc_t xr = make_rsrc(x + m0 * in);
+  uint32_t xoff[XP];
 #pragma unroll
   for (int i = 0; i < XP; ++i) {
     const int p = tid + i * kPrefillThreads;
-    const int64_t m = m0 + (p >> 2);
-    xok[i] = m < M;
-    xrow[i] = x + (xok[i] ? m : 0) * in + 8 * (p & 3);
+    xoff[i] = m0 + (p >> 2) < M ? (uint32_t)(((p >> 2) * in + 8 * (p & 3)) * 2) : kBufOOB;
   }
 
-  u32x4_t xq[2][XP];           // x pieces of the next two k-steps
-  u32x4_t idq[2][S][NV];       // index bytes of the current and next group of 4 k-steps
+  u32x4_t xq[4][XP];      // x pieces of steps k + 2 .. k + 5 (slot = step & 3)
+  u32x4_t idq[2][S][NV];  // index bytes of the current and next group of 4 k-steps
+  // Loads are issued unconditionally (a step or group past the end gets an
+  // out-of-range offset and reads zeros), so the body of a k-step is one
+  // basic block and the compiler's load counters stay exact.
   auto load_x = [&](int k, u32x4_t (&dst)[XP]) {
+    const uint32_t step = k < nk ? (uint32_t)(k * PBK * 2) : kBufOOB;
 #pragma unroll
-    for (int i = 0; i < XP; ++i) dst[i] = xok[i] ? ldg128(xrow[i] + k * PBK) : u32x4_t{0, 0, 0, 0};
+    for (int i = 0; i < XP; ++i) dst[i] = ldbuf128(xr, xoff[i] == kBufOOB ? kBufOOB : xoff[i] + step);
   };
   auto load_ids = [&](int grp, u32x4_t (&dst)[S][NV]) {
+    const uint32_t off = grp * 4 < nk ? idrow + (uint32_t)(grp * 16 * NV) : kBufOOB;
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int v = 0; v < NV; ++v) dst[s][v] = ldg128(reinterpret_cast<const uint8_t*>(idp[s] + grp * 16) + 16 * v);
+      for (int v = 0; v < NV; ++v) dst[s][v] = ldbuf128(idr[s], off == kBufOOB ? kBufOOB : off + 16 * v);
   };
   auto store_x = [&](int buf, const u32x4_t (&src)[XP]) {
 #pragma unroll
@@ -107,23 +167,19 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
       *reinterpret_cast<u32x4_t*>(xs + (buf * BM + (p >> 2)) * PSTR + 8 * (p & 3)) = src[i];
     }
   };
-  auto dequant = [&](int k, int buf, const u32x4_t (&ids)[S][NV]) {
-    const int tstep = k & 3;
+  auto block_ids = [&](int k, int b, const u32x4_t (&ids)[S][NV], uint32_t (&id)[S]) {
+    const int t = 4 * (k & 3) + 2 * wh + b;  // block inside the 16-block index group
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int t = 4 * tstep + 2 * wh + b;  // block inside the 16-block index group
-      uint32_t id[S];
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        uint32_t v;
-        if constexpr (NV == 1) v = (ids[s][0][t >> 2] >> (8 * (t & 3))) & 0xffu;
-        else v = (ids[s][t >> 3][(t >> 1) & 3] >> (16 * (t & 1))) & 0xffffu;
-        id[s] = min(v, kmax);
+    for (int s = 0; s < S; ++s) {
+      if constexpr (NV == 1) {
+        id[s] = (ids[s][0][t >> 2] >> (8 * (t & 3))) & 0xffu;  // inside the allocation
+      } else {
+        id[s] = min((ids[s][t >> 3][(t >> 1) & 3] >> (16 * (t & 1))) & 0xffffu, kmax);
       }
-      u32x4_t w = make_wfrag<S, LMODE, SEM, XDT>(lds_cb, id, K, L.active_mask, rs);
-      if (!w_row_ok) w = u32x4_t{0, 0, 0, 0};
-      *reinterpret_cast<u32x4_t*>(ws + (buf * PBN + wr_l) * PSTR + 8 * (2 * wh + b)) = w;
     }
+  };
+  auto store_w = [&](int buf, int b, const u32x4_t& w) {
+    *reinterpret_cast<u32x4_t*>(ws + (buf * PBN + wr_l) * PSTR + 8 * (2 * wh + b)) = w;
   };
 
   f32x4_t acc[TM][4];
@@ -132,48 +188,77 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // prologue: index group 0 (and 1), x of steps 0 and 1
-  load_ids(0, idq[0]);
-  if (nk > 4) load_ids(1, idq[1]);
-  load_x(0, xq[0]);
-  if (nk > 1) load_x(1, xq[1]);
-  __syncthreads();  // codebooks staged
-  dequant(0, 0, idq[0]);
-  store_x(0, xq[0]);
-  if (nk > 2) load_x(2, xq[0]);
-  __syncthreads();
-
+  // Pipeline (iteration k): the MFMAs of step k run on operand fragments
+  // already in registers while the fragments of step k + 1 are read from LDS
+  // buffer (k + 1) & 1 and step k + 2 is dequantised and copied into buffer
+  // k & 1, whose fragments every wave read into registers before the
+  // previous barrier.  One barrier per step.
+  auto produce = [&](int k, int buf, const u32x4_t (&ids)[S][NV], const u32x4_t (&xv)[XP]) {
+    uint32_t id0[S], id1[S];
+    block_ids(k, 0, ids, id0);
+    block_ids(k, 1, ids, id1);
+    const WfragRaw<S, LMODE> r0 = gather_wfrag_rep<S, LMODE>(lds_lane, id0, K, rshift);
+    const WfragRaw<S, LMODE> r1 = gather_wfrag_rep<S, LMODE>(lds_lane, id1, K, rshift);
+    store_w(buf, 0, combine_wfrag<S, LMODE, SEM, XDT>(r0, L.active_mask, rs));
+    store_w(buf, 1, combine_wfrag<S, LMODE, SEM, XDT>(r1, L.active_mask, rs));
+    store_x(buf, xv);
+  };
   const uint16_t* xa = xs + (wm * 16 * TM + l16) * PSTR + 8 * q;
   const uint16_t* wb = ws + (wn * 64 + l16) * PSTR + 8 * q;
+  u32x4_t fa[2][TM], fb[2][4];  // operand fragments of two steps
+  auto read_frags = [&](int buf, u32x4_t (&a)[TM], u32x4_t (&b)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(wb + (buf * PBN + j * 16) * PSTR);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const u32x4_t*>(xa + (buf * BM + i * 16) * PSTR);
+  };
+
+  // prologue: steps 0 and 1 into buffers 0 and 1, fragments of step 0
+  load_ids(0, idq[0]);
+  load_ids(1, idq[1]);
+  load_x(0, xq[0]);
+  load_x(1, xq[1]);
+  __syncthreads();  // codebooks staged
+  load_x(2, xq[2]);
+  load_x(3, xq[3]);
+  produce(0, 0, idq[0], xq[0]);
+  produce(1, 1, idq[0], xq[1]);
+  load_x(4, xq[0]);
+  load_x(5, xq[1]);
+  __syncthreads();
+  read_frags(0, fa[0], fb[0]);
+  __syncthreads();  // every wave holds step 0: buffer 0 may be refilled
+
   // Unrolled by 8 k-steps (two index groups) so that every register-array
-  // index below is a compile-time constant: k0 is a multiple of 8, so the
-  // buffer of step k is u & 1 and the index slot of group k / 4 is (u >> 2) & 1.
+  // index below is a compile-time constant: k0 is a multiple of 8, so step k
+  // uses fragment set u & 1 and, for step k + 2, the x slot (u + 2) & 3 and
+  // the index slot ((u + 2) >> 2) & 1.  x runs four steps ahead.
   for (int k0 = 0; k0 < nk; k0 += 8) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int k = k0 + u;
       if (k >= nk) break;  // uniform
-      const int cur = u & 1;
-      // MFMAs of step k (operands from buffer cur)
-      u32x4_t b[4];
+      const int c = u & 1;
+      const int gs2 = ((u + 2) >> 2) & 1;
+      // fragments of step k + 1 (past the end: unused)
+      read_frags(c ^ 1, fa[c ^ 1], fb[c ^ 1]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(wb + (cur * PBN + j * 16) * PSTR);
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa + (cur * BM + i * 16) * PSTR);
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<XDT>(fa[c][i], fb[c][j], acc[i][j]);
+      // step k + 2 into buffer c (past the end: harmless)
+      produce(k + 2, c, idq[gs2], xq[(u + 2) & 3]);
+      load_x(k + 6, xq[(u + 2) & 3]);
+      // once the last step of a group is produced, the group two ahead goes
+      // into its slot
+      if (((u + 2) & 3) == 3) load_ids(((k + 2) >> 2) + 2, idq[gs2]);
+      // issue order: LDS reads (fragments, codewords), then the MFMAs, each
+      // followed by a share of the dequantisation arithmetic
+      __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4 + TM + S * (LMODE == LM_F32 ? 4 : 2), 0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<XDT>(a, b[j], acc[i][j]);
-      }
-      // produce step k + 1 into buffer cur ^ 1 while the MFMAs run
-      if (k + 1 < nk) {
-        const int gs = ((u + 1) >> 2) & 1;  // index slot of group (k + 1) / 4
-        dequant(k + 1, cur ^ 1, idq[gs]);
-        store_x(cur ^ 1, xq[(u + 1) & 1]);
-        if (k + 3 < nk) load_x(k + 3, xq[(u + 1) & 1]);
-        // after the last step of a group is dequantised, the group two ahead
-        // goes into its slot
-        const int g = (k + 1) >> 2;
-        if (((u + 1) & 3) == 3 && (g + 2) * 4 < nk) load_ids(g + 2, idq[gs]);
+      for (int i = 0; i < TM * 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSgValu, 3, 0);
       }
       __syncthreads();
     }
@@ -198,7 +283,14 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int TM>
 static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
                              int64_t M, hipStream_t st) {
-  const size_t lds = prefill_lds_bytes<S, LMODE>(TM, L.codebook_size);
+  // as many table copies (up to 8) as fit; the compact table is staged in
+  // the W tile area first, so replication needs it to fit there
+  const size_t tbl = (size_t)prefill_table_entries<S, IdT>(L.codebook_size) * lds_entry_bytes<LMODE>();
+  int rshift = 3;
+  while (rshift > 0 && (prefill_lds_bytes<S, IdT, LMODE>(TM, L.codebook_size, rshift) > (size_t)160 * 1024 ||
+                        tbl > (size_t)2 * PBN * PSTR * sizeof(uint16_t)))
+    --rshift;
+  const size_t lds = prefill_lds_bytes<S, IdT, LMODE>(TM, L.codebook_size, rshift);
   auto kern = rvq_prefill_kernel<S, IdT, LMODE, SEM, XDT, TM>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -210,7 +302,7 @@ static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const Epilo
   const int n_mt = (int)((M + prefill_bm<TM>() - 1) / prefill_bm<TM>());
   dim3 grid((unsigned)(L.n_tiles * (int64_t)n_mt));
   hipLaunchKernelGGL(kern, grid, dim3(kPrefillThreads), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M,
-                     n_mt);
+                     n_mt, rshift);
   return hipGetLastError();
 }
 
