@@ -13,12 +13,12 @@
 //     [64c + 16q, 64c + 16q + 16), q = l / 16: one 128-bit load per stage for
 //     8-bit ids, two for 16-bit ids.
 //   * Software pipeline: the index loads (and the lane's row-scale load) of
-//     the item PF slots ahead are issued right after an item is consumed, as
-//     straight-line code into a fixed register ring, so the hardware keeps PF
-//     items of loads in flight per wave and the only memory waits in the loop
-//     are the in-order ones for the slot being consumed.  Loads past the end
-//     of the range are clamped to a valid address and their results unused.
-//     Per-tile metadata comes from the plan through the scalar cache.
+//     the item PF slots ahead (decode_prefetch) are issued right after an
+//     item is consumed, as straight-line code into a fixed register ring, so
+//     the only memory waits in the loop are the in-order ones for the slot
+//     being consumed.  Loads past the end of the range get an out-of-range
+//     buffer offset and read zeros without touching memory.  Per-tile
+//     metadata comes from the plan through the scalar cache.
 //   * For each block the lane gathers the S codewords from LDS, rebuilds the 8
 //     weights exactly as the reference's dequantisation does (rvq_fragment.h)
 //     and feeds them as the B operand of v_mfma_f32_16x16x32_{bf16,f16}; the A
@@ -42,11 +42,14 @@ namespace wal {
 constexpr int kDecodeMaxWaves = 8;
 constexpr int kDecodeMaxThreads = kDecodeMaxWaves * 64;
 
-// Items of index loads in flight per wave: about 128 bytes per lane.
+// Items of index loads in flight per wave.  Measured on gfx950 at every
+// benchmark shape (c2, c3, c5): one item ahead is fastest.  The loop is bound
+// by the LDS codeword gathers and the dequantisation arithmetic, not by HBM
+// latency, and every deeper ring slot adds straight-line code and prologue
+// loads (PF 4 -> 1: c3 +4 %, c5 +8 %, c2 +5 % tokens/s).
 template <int S, typename IdT>
 constexpr int decode_prefetch() {
-  constexpr int w = S * (int)sizeof(IdT);
-  return w <= 1 ? 8 : (w <= 2 ? 4 : (w <= 3 ? 3 : 2));
+  return 1;
 }
 
 template <typename IdT>
