@@ -212,6 +212,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   const bool have_image = L.image != nullptr;
   const uint8_t* img0 = have_image ? L.image + (size_t)cti.group * tbl_bytes : nullptr;
   const uint8_t* img1 = have_image ? L.image + (size_t)sti.group * tbl_bytes : nullptr;
+  const bool same_img = sti.group == cti.group;
   const int n16 = XLDS ? M * in / 8 : 0;  // 16-byte pieces of x (in % 128 == 0)
   const int t16 = tbl_bytes / 16;
   u32x4_t xr[XR];
@@ -220,7 +221,9 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   u32x4_t b0[kImageBatch], b1[kImageBatch];
   if (have_image) {
     load_image_batch(b0, img0, t16, tid, blockDim.x);
-    if (two) load_image_batch(b1, img1, t16, tid, blockDim.x);
+    // both slots of one group (two scale runs) stage from the same image:
+    // load it once (per-CU load bandwidth bounds this prologue)
+    if (two && !same_img) load_image_batch(b1, img1, t16, tid, blockDim.x);
   }
   uint32_t sc0 = 0, sc1 = 0;  // scales of the two segments (scaled tables)
   if constexpr (SCALED) {
@@ -269,7 +272,15 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   }
   if (have_image) {
     stage_image<XDT, SCALED>(lds_cb, img0, t16, r0, &b0);
-    if (two) stage_image<XDT, SCALED>(lds_cb + tbl_bytes, img1, t16, r1, &b1);
+    if (two) {
+      // (a register copy: selecting between the two arrays by pointer would
+      // put both in scratch memory)
+      if (same_img) {
+#pragma unroll
+        for (int u = 0; u < kImageBatch; ++u) b1[u] = b0[u];
+      }
+      stage_image<XDT, SCALED>(lds_cb + tbl_bytes, img1, t16, r1, &b1);
+    }
   } else {
     // no image: convert the raw codebooks here (out of line)
     stage_table<S, LMODE, SEM, XDT, SCALED>(0u, nullptr, cti.p, K, D, r0);
