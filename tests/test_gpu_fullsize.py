@@ -1,0 +1,79 @@
+"""GPU parity at the benchmark configurations' full sizes.
+
+Whole weight matrices of the real shapes (Llama-3-8B gate_proj for c3 and c4,
+Qwen2.5-7B gate_proj for c5) are checked against the CPU oracle:
+* the dequantised weight bit for bit (the whole matrix);
+* decode outputs (M = 1) in fp32 against the float64 contraction of the
+  oracle's weight, max|dy| / max|y| <= 2e-3;
+* prefill outputs (M = 2048) on a sample of activation rows, same bar (the
+  oracle's float64 contraction of every row would take minutes);
+* linearity of the decode kernel over the full matrix:
+  y(x1 + x2) = y(x1) + y(x2) up to fp32 accumulation.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from _cases import bits, module_buffers_as_encoding, oracle_weight, rel_err
+from oracle import c_oracle
+from wal2026_amd import PackedGroupedBlockRVQLinear, synth
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+SHAPES = [
+    ("c3_gate", "c3", 14336, 4096),
+    ("c4_gate", "c4", 14336, 4096),
+    ("c5_gate", "c5", 18944, 3584),
+]
+
+
+def _layer(cname, out_f, in_f, dev, seed=0):
+    cfg = synth.CONFIGS[cname]
+    gen = synth.generator(seed)
+    enc = synth.make_encoding(out_f, in_f, cfg, gen)
+    return cfg, PackedGroupedBlockRVQLinear(enc, matmul_strategy="hip_block_rvq").to(dev), gen
+
+
+@pytest.mark.parametrize("name,cname,out_f,in_f", SHAPES, ids=[s[0] for s in SHAPES])
+def test_full_weight_bitexact(name, cname, out_f, in_f, gpu_device):
+    print(f"[fullsize] reconstruct {name} {out_f}x{in_f}", flush=True)
+    cfg, mod, _ = _layer(cname, out_f, in_f, gpu_device)
+    got = mod.reconstruct_weight(cfg.x_dtype).cpu()
+    want = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
+    assert torch.equal(bits(got), bits(want)), name
+
+
+@pytest.mark.parametrize("name,cname,out_f,in_f", [s for s in SHAPES if s[1] != "c4"],
+                         ids=[s[0] for s in SHAPES if s[1] != "c4"])
+def test_full_decode_parity_and_linearity(name, cname, out_f, in_f, gpu_device):
+    print(f"[fullsize] decode {name}", flush=True)
+    cfg, mod, gen = _layer(cname, out_f, in_f, gpu_device)
+    x = synth.make_activation(1, in_f, cfg.x_dtype, gen)
+    y = mod._hip_linear(x.to(gpu_device), fast=False, out_dtype=torch.float32)
+    w_ref = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
+    assert rel_err(y, c_oracle.linear_f64(x, w_ref)) <= TOL, name
+    # linearity: x1 and x2 chosen so that x1 + x2 is exact in bf16 (disjoint
+    # supports), so y(x1 + x2) and y(x1) + y(x2) differ only by fp32 sums
+    x1 = x.clone()
+    x1[:, in_f // 2:] = 0
+    x2 = x - x1
+    dev = gpu_device
+    y1 = mod._hip_linear(x1.to(dev), fast=False, out_dtype=torch.float32)
+    y2 = mod._hip_linear(x2.to(dev), fast=False, out_dtype=torch.float32)
+    assert rel_err(y1 + y2, y) <= 1e-5, name
+
+
+def test_full_prefill_parity_sampled_rows(gpu_device):
+    """c4: S = 2, K = 256, 8-bit ids, bf16 x, M = 2048 through the prefill
+    kernel; 24 sampled rows of y against the oracle."""
+    print("[fullsize] prefill c4 gate 2048x14336x4096", flush=True)
+    cfg, mod, gen = _layer("c4", 14336, 4096, gpu_device)
+    x = synth.make_activation(2048, 4096, cfg.x_dtype, gen)
+    y = mod._hip_linear(x.to(gpu_device), fast=False, out_dtype=torch.float32).cpu()
+    rows = torch.randperm(2048, generator=torch.Generator().manual_seed(5))[:24]
+    rows = torch.cat([rows, torch.tensor([0, 127, 128, 2047])])
+    w_ref = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
+    ref = c_oracle.linear_f64(x[rows], w_ref)
+    assert rel_err(y[rows], ref) <= TOL
