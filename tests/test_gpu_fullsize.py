@@ -45,12 +45,18 @@ def test_full_weight_bitexact(name, cname, out_f, in_f, gpu_device):
     assert torch.equal(bits(got), bits(want)), name
 
 
-@pytest.mark.parametrize("name,cname,out_f,in_f", [s for s in SHAPES if s[1] != "c4"],
-                         ids=[s[0] for s in SHAPES if s[1] != "c4"])
-def test_full_decode_parity_and_linearity(name, cname, out_f, in_f, gpu_device):
-    print(f"[fullsize] decode {name}", flush=True)
+DECODE_CASES = [(s, m) for s in SHAPES if s[1] != "c4" for m in ((1, 4, 16) if s[1] == "c3" else (1,))]
+
+
+@pytest.mark.parametrize("shape,m", DECODE_CASES, ids=[f"{s[0]}_m{m}" for s, m in DECODE_CASES])
+def test_full_decode_parity_and_linearity(shape, m, gpu_device):
+    """M = 1, 4, 16 at c3 cover the three decode layouts the launch planner
+    picks there (x in LDS with two table slots; x from global memory into
+    registers with two slots; the same with one slot)."""
+    name, cname, out_f, in_f = shape
+    print(f"[fullsize] decode {name} m={m}", flush=True)
     cfg, mod, gen = _layer(cname, out_f, in_f, gpu_device)
-    x = synth.make_activation(1, in_f, cfg.x_dtype, gen)
+    x = synth.make_activation(m, in_f, cfg.x_dtype, gen)
     y = mod._hip_linear(x.to(gpu_device), fast=False, out_dtype=torch.float32)
     w_ref = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
     assert rel_err(y, c_oracle.linear_f64(x, w_ref)) <= TOL, name

@@ -143,8 +143,10 @@ __device__ __attribute__((noinline)) void stage_table(uint32_t dst_off, const ui
 enum XMode : int {
   XM_GLOBAL = 0,  // x does not fit in LDS: read per item from global memory (L2)
   XM_LDS = 1,     // x staged in LDS, fragments read per item
-  XM_REG = 2      // x staged in LDS; each wave owns one chunk (CPT == 1), so its
+  XM_REG = 2,     // x staged in LDS; each wave owns one chunk (CPT == 1), so its
                   // 16 fragments are read once and kept in registers
+  XM_GREG = 3     // as XM_REG, but the 16 fragments come straight from global
+                  // memory (large M: x beside two tables would not fit LDS)
 };
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int XMODE, bool SCALED>
@@ -157,7 +159,8 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   // of a line is its own dependent scalar-memory round trip.
   asm volatile("" ::"s"(L.in_features), "s"(L.plan), "s"(L.g0.stage_ids[0]), "s"(L.g0.codebooks[4]),
                "s"(L.g0.row_scale), "s"(L.image), "s"(D.x_dtype), "s"(E.y), "s"(E.bias_mode), "s"(x), "s"(nslots));
-  constexpr bool XLDS = XMODE != XM_GLOBAL;
+  constexpr bool XLDS = XMODE == XM_LDS || XMODE == XM_REG;
+  constexpr bool XREG = XMODE == XM_REG || XMODE == XM_GREG;
   constexpr int PF = decode_prefetch<S, IdT>(), NV = sizeof(IdT);
   constexpr int ESZ = lds_entry_bytes<LMODE>();
   constexpr int XR = 4;  // 16-byte x loads per thread kept in registers across the codebook staging
@@ -218,6 +221,16 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   u32x4_t xr[XR];
 #pragma unroll
   for (int u = 0; u < XR; ++u) xr[u] = ldg128(x + (size_t)min(tid + u * (int)blockDim.x, max(n16 - 1, 0)) * 8);
+  // XM_REG / XM_GREG: this wave's chunk is the same for every tile, so its 16
+  // x fragments (zero past the row) are read once: XM_GREG here, from global
+  // memory, XM_REG after the barrier, from the x rows staged in LDS.
+  u32x4_t xreg[XREG ? 16 : 1];
+  if constexpr (XMODE == XM_GREG) {
+    const int base = wave * 64 + 16 * q;
+#pragma unroll
+    for (int tt = 0; tt < 16; ++tt)
+      xreg[tt] = base < B ? ldg128(x + (size_t)xm * in + (size_t)(base + tt) * 8) : u32x4_t{0, 0, 0, 0};
+  }
   u32x4_t b0[kImageBatch], b1[kImageBatch];
   if (have_image) {
     load_image_batch(b0, img0, t16, tid, blockDim.x);
@@ -295,16 +308,15 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   }
   __syncthreads();
 
-  // XM_REG: this wave's chunk is the same for every tile; read its 16 x
-  // fragments (zero past the row) once.
-  u32x4_t xreg[XMODE == XM_REG ? 16 : 1];
   if constexpr (XMODE == XM_REG) {
     const int base = wave * 64 + 16 * q;
     const uint8_t* xp = base < B ? reinterpret_cast<const uint8_t*>(xs + (size_t)xm * in + (size_t)base * 8) : zrow;
 #pragma unroll
     for (int tt = 0; tt < 16; ++tt) xreg[tt] = *reinterpret_cast<const u32x4_t*>(xp + tt * 16);
+  }
+  if constexpr (XREG) {
     // Opaque to the compiler, so it keeps them in registers instead of
-    // re-reading LDS next to each MFMA (waiting on the newest LDS read is a
+    // re-reading them next to each MFMA (waiting on the newest LDS read is a
     // full lgkmcnt(0) wait, which would serialise the gathers).
 #pragma unroll
     for (int tt = 0; tt < 16; ++tt) asm volatile("" : "+v"(xreg[tt]));
@@ -368,7 +380,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
 #pragma unroll
         for (int tt = 0; tt < 16; ++tt) {
           u32x4_t xf;
-          if constexpr (XMODE == XM_REG) {
+          if constexpr (XREG) {
             xf = xreg[tt];
           } else if constexpr (XMODE == XM_LDS) {
             xf = *reinterpret_cast<const u32x4_t*>(xp + tt * 16);
@@ -430,33 +442,41 @@ static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const Epilog
     *share = (L.n_tiles + g - 1) / g;
     return true;
   };
-  // Two table slots when a workgroup's tiles can span two tables (several
-  // groups, or scaled tables with more than one scale run) and they fit with
-  // x in LDS; else one slot (a second table is restaged in the loop).
+  // Candidate layouts in order of preference; the first whose grid fits one
+  // round of workgroups (one per CU) wins, else the one with the fewest
+  // rounds.  Two table slots when a workgroup's tiles can span two tables
+  // (several groups, or scaled tables with more than one scale run); x in
+  // LDS, or in registers straight from global memory when each wave owns one
+  // chunk (large M, where x beside the tables would not fit), or read per
+  // item from global memory.
   const bool segments = L.plan != nullptr || SCALED;
-  int grid = 0, share = 1, nslots = 0;
-  bool xlds = true;
-  for (const int ns : {2, 1}) {
-    if (ns == 2 && !segments) continue;
-    if (plan_for(ns, true, &grid, &share)) { nslots = ns; break; }
-  }
-  if (nslots == 0) {
-    xlds = false;
-    for (const int ns : {2, 1}) {
-      if (ns == 2 && !segments) continue;
-      if (plan_for(ns, false, &grid, &share)) { nslots = ns; break; }
+  const int nchunk = (L.blocks_per_row + 63) / 64;
+  const bool one_chunk = nchunk <= nw;
+  struct Cand { int xmode, nslots; };
+  const Cand cands[] = {{one_chunk ? XM_REG : XM_LDS, 2}, {XM_GREG, 2}, {one_chunk ? XM_REG : XM_LDS, 1},
+                        {XM_GREG, 1}, {XM_GLOBAL, 2}, {XM_GLOBAL, 1}};
+  int grid = 0, share = 1, nslots = 0, xmode = XM_GLOBAL, best_rounds = 1 << 30;
+  for (const Cand& c : cands) {
+    if (c.nslots == 2 && !segments) continue;
+    if (c.xmode == XM_GREG && !one_chunk) continue;
+    int g = 0, sh = 1;
+    if (!plan_for(c.nslots, c.xmode == XM_REG || c.xmode == XM_LDS, &g, &sh)) continue;
+    const int rounds = (g + n_cu - 1) / n_cu;
+    if (rounds < best_rounds) {
+      best_rounds = rounds;
+      grid = g; share = sh; nslots = c.nslots; xmode = c.xmode;
     }
+    if (rounds <= 1) break;
   }
   if (nslots == 0) return hipErrorInvalidValue;  // excluded by the host's eligibility check
+  const bool xlds = xmode == XM_REG || xmode == XM_LDS;
   const size_t lds = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, share, nslots);
   if (grid < 1) return hipSuccess;
-  // one chunk per wave -> activation fragments stay in registers
-  const int nchunk = (L.blocks_per_row + 63) / 64;
-  const int xmode = !xlds ? XM_GLOBAL : (nchunk <= nw ? XM_REG : XM_LDS);
-  auto kern = xmode == XM_REG ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_REG, SCALED>
-              : xmode == XM_LDS ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_LDS, SCALED>
-                                : rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GLOBAL, SCALED>;
-  static bool attr_set[3] = {false, false, false};
+  auto kern = xmode == XM_REG    ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_REG, SCALED>
+              : xmode == XM_LDS  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_LDS, SCALED>
+              : xmode == XM_GREG ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GREG, SCALED>
+                                 : rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GLOBAL, SCALED>;
+  static bool attr_set[4] = {false, false, false, false};
   if (!attr_set[xmode]) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                        kLdsMax);
