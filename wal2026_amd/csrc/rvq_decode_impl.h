@@ -220,7 +220,12 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   const int t16 = tbl_bytes / 16;
   u32x4_t xr[XR];
 #pragma unroll
-  for (int u = 0; u < XR; ++u) xr[u] = ldg128(x + (size_t)min(tid + u * (int)blockDim.x, max(n16 - 1, 0)) * 8);
+  for (int u = 0; u < XR; ++u) {
+    // (uniform: n16 is a multiple of 64) no load for pieces past x, which
+    // would only take load-issue bandwidth from the table loads behind them
+    if (u == 0 || u * (int)blockDim.x < n16)
+      xr[u] = ldg128(x + (size_t)min(tid + u * (int)blockDim.x, max(n16 - 1, 0)) * 8);
+  }
   // XM_REG / XM_GREG: this wave's chunk is the same for every tile, so its 16
   // x fragments (zero past the row) are read once: XM_GREG here, from global
   // memory, XM_REG after the barrier, from the x rows staged in LDS.
