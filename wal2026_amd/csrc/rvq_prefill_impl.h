@@ -39,7 +39,10 @@
 
 namespace wal {
 
-constexpr int kPrefillThreads = 512;
+constexpr int kConsumerWaves = 8;   // MFMA waves
+constexpr int kProducerWaves = 8;   // dequantisation and x-copy waves
+constexpr int kPrefillThreads = (kConsumerWaves + kProducerWaves) * 64;
+constexpr int kProducerThreads = kProducerWaves * 64;
 constexpr int PBN = 256;        // weight rows per workgroup tile
 constexpr int PBK = 32;         // k per step
 constexpr int PSTR = PBK + 16;  // elements per LDS row (96 bytes; see below)
@@ -67,17 +70,17 @@ WAL_HOST_DEVICE size_t prefill_lds_bytes(int TM, int K, int rshift) {
          ((size_t)prefill_table_entries<S, IdT>(K) * lds_entry_bytes<LMODE>() << rshift);
 }
 
-// sched_group_barrier masks
-constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgDsRead = 0x100, kSgDsWrite = 0x200, kSgVmemRead = 0x020;
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int TM>
 __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
                                                                       const uint16_t* __restrict__ x, int64_t M,
                                                                       int n_mt, int rshift) {
   constexpr int BM = prefill_bm<TM>();
-  constexpr int XP = BM * 4 / kPrefillThreads;  // 16-byte x pieces per thread per k-step (1 or 2)
-  constexpr int NV = sizeof(IdT);                // 16-byte index loads per stage per group of 4 k-steps
-  static_assert(XP >= 1 && BM * 4 % kPrefillThreads == 0, "x tile split");
+  constexpr int XP = BM * 4 / kProducerThreads;  // 16-byte x pieces per producer thread per k-step
+  constexpr int BPT = PBN * 4 / kProducerThreads;  // blocks each producer thread dequantises per k-step
+  constexpr int NV = sizeof(IdT);                  // 16-byte index loads per stage per group of 4 k-steps
+  static_assert(XP >= 1 && BM * 4 % kProducerThreads == 0, "x tile split");
+  static_assert(BPT == 2, "two producer threads per weight row");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [2][BM][PSTR]
   uint16_t* ws = xs + 2 * BM * PSTR;                 // [2][PBN][PSTR]
@@ -87,8 +90,6 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
-  const int l16 = lane & 15, q = lane >> 4;
   const int mt = (int)(blockIdx.x % (unsigned)n_mt);
   const int nt = (int)(blockIdx.x / (unsigned)n_mt);
   const FragTile<S> ti = get_frag_tile<S>(L, nt);
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
 
   // Codebook table, replicated 1 << rshift times (host choice: as many
   // copies, up to 8, as LDS holds): staged compactly into the idle W tile
-  // area, then spread into the replicated layout.
+  // area, then spread into the replicated layout.  All waves take part.
   constexpr int ESZ = lds_entry_bytes<LMODE>();
   if (rshift == 0) {
     stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, ti.p, K, D);
@@ -117,13 +118,59 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
           *reinterpret_cast<const u32x4_t*>(compact + (size_t)piece * 16);
     }
   }
-  const uint8_t* lds_lane = lds_cb + (lane & ((1 << rshift) - 1)) * ESZ;  // this lane's copy
+  __syncthreads();  // table staged (and the compact copy in the W area read)
 
-  // dequantiser role: weight row wr_l, blocks 2 * wh + {0, 1} of every k-step.
+  if (wave < kConsumerWaves) {
+    // ---- consumers: 8 waves (2 per SIMD, the pair that keeps the matrix
+    // core busy), 2 (M) x 4 (N), each a 16 TM x 64 output tile ----
+    const int wm = wave >> 2, wn = wave & 3;
+    const int l16 = lane & 15, q = lane >> 4;
+    const uint16_t* xa = xs + (wm * 16 * TM + l16) * PSTR + 8 * q;
+    const uint16_t* wb = ws + (wn * 64 + l16) * PSTR + 8 * q;
+    f32x4_t acc[TM][4];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();  // step 0 produced
+    for (int k = 0; k < nk; ++k) {
+      const int buf = k & 1;
+      u32x4_t a[TM], b[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(wb + (buf * PBN + j * 16) * PSTR);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const u32x4_t*>(xa + (buf * BM + i * 16) * PSTR);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<XDT>(a[i], b[j], acc[i][j]);
+      __syncthreads();  // buffer buf read; step k + 1 produced
+    }
+    // lane holds D[m = 4q + e][n = l16] of each 16 x 16 tile
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int nloc = wn * 64 + j * 16 + l16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t m = m0 + wm * 16 * TM + i * 16 + 4 * q + e;
+          if (m < M && nloc < ti.rows) store_output(E, m, ti.out_row0 + nloc, acc[i][j][e]);
+        }
+      }
+    }
+    return;
+  }
+
+  // ---- producers: 8 waves (two per SIMD, running beside the MFMAs of the
+  // two consumer waves there); threads pt = 2r, 2r + 1 own weight row r,
+  // blocks 2 (pt & 1) + {0, 1} of every k-step ----
+  const int pt = tid - kConsumerWaves * 64;
+  const int prow = pt >> 1, ph = pt & 1;
+  const uint8_t* lds_lane = lds_cb + (lane & ((1 << rshift) - 1)) * ESZ;  // this lane's table copy
   // Rows past the tile dequantise the tile's first row; their outputs are
   // never stored.
-  const int wr_l = tid >> 1, wh = tid & 1;
-  const int64_t wr = ti.row0 + (wr_l < ti.rows ? wr_l : 0);
+  const int64_t wr = ti.row0 + (prow < ti.rows ? prow : 0);
   const RowScale rs = make_row_scale<XDT>(load_f(ti.p.row_scale, D.sc_dtype, scale_index(L, wr)));
   // index planes: one descriptor per stage on the group's base (uniform; a
   // per-lane base would make the compiler loop over the lanes' descriptors),
@@ -132,22 +179,18 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
 #pragma unroll
   for (int s = 0; s < S; ++s) idr[s] = make_rsrc(ti.p.ids[s]);
   const uint32_t idrow = (uint32_t)(wr * B * (int64_t)sizeof(IdT));
-
-  // x loader role: piece p = tid + i * 512 -> row p / 4, 16-byte column p % 4,
-  // addressed from the tile's first row (rows past M read zeros)
+  // x pieces p = pt + i * 256 -> row p / 4, 16-byte column p % 4, addressed
+  // from the tile's first row (rows past M read zeros)
   const bufrsrc_t xr = make_rsrc(x + m0 * in);
   uint32_t xoff[XP];
 #pragma unroll
   for (int i = 0; i < XP; ++i) {
-    const int p = tid + i * kPrefillThreads;
+    const int p = pt + i * kProducerThreads;
     xoff[i] = m0 + (p >> 2) < M ? (uint32_t)(((p >> 2) * in + 8 * (p & 3)) * 2) : kBufOOB;
   }
-
-  u32x4_t xq[4][XP];      // x pieces of steps k + 2 .. k + 5 (slot = step & 3)
-  u32x4_t idq[2][S][NV];  // index bytes of the current and next group of 4 k-steps
-  // Loads are issued unconditionally (a step or group past the end gets an
-  // out-of-range offset and reads zeros), so the body of a k-step is one
-  // basic block and the compiler's load counters stay exact.
+  // Loads are unconditional (a step or group past the end gets an
+  // out-of-range offset and reads zeros), so a step is one basic block and
+  // the compiler's load counters stay exact.
   auto load_x = [&](int k, u32x4_t (&dst)[XP]) {
     const uint32_t step = k < nk ? (uint32_t)(k * PBK * 2) : kBufOOB;
 #pragma unroll
@@ -160,122 +203,60 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
 #pragma unroll
       for (int v = 0; v < NV; ++v) dst[s][v] = ldbuf128(idr[s], off == kBufOOB ? kBufOOB : off + 16 * v);
   };
-  auto store_x = [&](int buf, const u32x4_t (&src)[XP]) {
+  // step k: the thread's 2 blocks into W buffer buf, x pieces into x buffer buf
+  auto produce = [&](int k, int buf, const u32x4_t (&ids)[S][NV], const u32x4_t (&xv)[XP]) {
+    WfragRaw<S, LMODE> raw[BPT];
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const int t = 4 * (k & 3) + 2 * ph + b;  // block inside the 16-block index group
+      uint32_t id[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        if constexpr (NV == 1) {
+          id[s] = (ids[s][0][t >> 2] >> (8 * (t & 3))) & 0xffu;  // inside the allocation
+        } else {
+          id[s] = min((ids[s][t >> 3][(t >> 1) & 3] >> (16 * (t & 1))) & 0xffffu, kmax);
+        }
+      }
+      raw[b] = gather_wfrag_rep<S, LMODE>(lds_lane, id, K, rshift);
+    }
+    uint16_t* wd = ws + (buf * PBN + prow) * PSTR + 16 * ph;
+#pragma unroll
+    for (int b = 0; b < BPT; ++b)
+      *reinterpret_cast<u32x4_t*>(wd + 8 * b) = combine_wfrag<S, LMODE, SEM, XDT>(raw[b], L.active_mask, rs);
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
-      const int p = tid + i * kPrefillThreads;
-      *reinterpret_cast<u32x4_t*>(xs + (buf * BM + (p >> 2)) * PSTR + 8 * (p & 3)) = src[i];
+      const int p = pt + i * kProducerThreads;
+      *reinterpret_cast<u32x4_t*>(xs + (buf * BM + (p >> 2)) * PSTR + 8 * (p & 3)) = xv[i];
     }
   };
-  auto block_ids = [&](int k, int b, const u32x4_t (&ids)[S][NV], uint32_t (&id)[S]) {
-    const int t = 4 * (k & 3) + 2 * wh + b;  // block inside the 16-block index group
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      if constexpr (NV == 1) {
-        id[s] = (ids[s][0][t >> 2] >> (8 * (t & 3))) & 0xffu;  // inside the allocation
-      } else {
-        id[s] = min((ids[s][t >> 3][(t >> 1) & 3] >> (16 * (t & 1))) & 0xffffu, kmax);
-      }
-    }
-  };
-  auto store_w = [&](int buf, int b, const u32x4_t& w) {
-    *reinterpret_cast<u32x4_t*>(ws + (buf * PBN + wr_l) * PSTR + 8 * (2 * wh + b)) = w;
-  };
 
-  f32x4_t acc[TM][4];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // Pipeline (iteration k): the MFMAs of step k run on operand fragments
-  // already in registers while the fragments of step k + 1 are read from LDS
-  // buffer (k + 1) & 1 and step k + 2 is dequantised and copied into buffer
-  // k & 1, whose fragments every wave read into registers before the
-  // previous barrier.  One barrier per step.
-  auto produce = [&](int k, int buf, const u32x4_t (&ids)[S][NV], const u32x4_t (&xv)[XP]) {
-    uint32_t id0[S], id1[S];
-    block_ids(k, 0, ids, id0);
-    block_ids(k, 1, ids, id1);
-    const WfragRaw<S, LMODE> r0 = gather_wfrag_rep<S, LMODE>(lds_lane, id0, K, rshift);
-    const WfragRaw<S, LMODE> r1 = gather_wfrag_rep<S, LMODE>(lds_lane, id1, K, rshift);
-    store_w(buf, 0, combine_wfrag<S, LMODE, SEM, XDT>(r0, L.active_mask, rs));
-    store_w(buf, 1, combine_wfrag<S, LMODE, SEM, XDT>(r1, L.active_mask, rs));
-    store_x(buf, xv);
-  };
-  const uint16_t* xa = xs + (wm * 16 * TM + l16) * PSTR + 8 * q;
-  const uint16_t* wb = ws + (wn * 64 + l16) * PSTR + 8 * q;
-  u32x4_t fa[2][TM], fb[2][4];  // operand fragments of two steps
-  auto read_frags = [&](int buf, u32x4_t (&a)[TM], u32x4_t (&b)[4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(wb + (buf * PBN + j * 16) * PSTR);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const u32x4_t*>(xa + (buf * BM + i * 16) * PSTR);
-  };
-
-  // prologue: steps 0 and 1 into buffers 0 and 1, fragments of step 0
+  u32x4_t xq[4][XP];      // x pieces of steps k + 1 .. k + 4 (slot = step & 3)
+  u32x4_t idq[2][S][NV];  // index bytes of two groups of 4 k-steps (slot = group & 1)
   load_ids(0, idq[0]);
   load_ids(1, idq[1]);
-  load_x(0, xq[0]);
-  load_x(1, xq[1]);
-  __syncthreads();  // codebooks staged
-  load_x(2, xq[2]);
-  load_x(3, xq[3]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) load_x(j, xq[j]);
   produce(0, 0, idq[0], xq[0]);
-  produce(1, 1, idq[0], xq[1]);
   load_x(4, xq[0]);
-  load_x(5, xq[1]);
-  __syncthreads();
-  read_frags(0, fa[0], fb[0]);
-  __syncthreads();  // every wave holds step 0: buffer 0 may be refilled
-
-  // Unrolled by 8 k-steps (two index groups) so that every register-array
-  // index below is a compile-time constant: k0 is a multiple of 8, so step k
-  // uses fragment set u & 1 and, for step k + 2, the x slot (u + 2) & 3 and
-  // the index slot ((u + 2) >> 2) & 1.  x runs four steps ahead.
+  __syncthreads();  // step 0 produced
+  // Iteration k produces step k + 1 into buffer (k + 1) & 1 (read by the
+  // consumers in iteration k - 1, before the previous barrier).  Unrolled by
+  // 8 so that register-array indices are compile-time constants (k0 is a
+  // multiple of 8): step k + 1 uses x slot (u + 1) & 3 and index slot
+  // ((u + 1) >> 2) & 1; x runs four steps ahead, index bytes a group ahead.
   for (int k0 = 0; k0 < nk; k0 += 8) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int k = k0 + u;
       if (k >= nk) break;  // uniform
-      const int c = u & 1;
-      const int gs2 = ((u + 2) >> 2) & 1;
-      // fragments of step k + 1 (past the end: unused)
-      read_frags(c ^ 1, fa[c ^ 1], fb[c ^ 1]);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<XDT>(fa[c][i], fb[c][j], acc[i][j]);
-      // step k + 2 into buffer c (past the end: harmless)
-      produce(k + 2, c, idq[gs2], xq[(u + 2) & 3]);
-      load_x(k + 6, xq[(u + 2) & 3]);
+      const int gs = ((u + 1) >> 2) & 1;
+      produce(k + 1, (u + 1) & 1, idq[gs], xq[(u + 1) & 3]);  // past the end: harmless
+      load_x(k + 5, xq[(u + 1) & 3]);
       // once the last step of a group is produced, the group two ahead goes
       // into its slot
-      if (((u + 2) & 3) == 3) load_ids(((k + 2) >> 2) + 2, idq[gs2]);
-      // issue order: LDS reads (fragments, codewords), then the MFMAs, each
-      // followed by a share of the dequantisation arithmetic
-      __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4 + TM + S * (LMODE == LM_F32 ? 4 : 2), 0);
-#pragma unroll
-      for (int i = 0; i < TM * 4; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSgValu, 3, 0);
-      }
+      if (((u + 1) & 3) == 3) load_ids(((k + 1) >> 2) + 2, idq[gs]);
       __syncthreads();
-    }
-  }
-
-  // lane holds D[m = 4q + e][n = l16] of each 16 x 16 tile
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int nloc = wn * 64 + j * 16 + l16;
-      if (nloc >= ti.rows) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t m = m0 + wm * 16 * TM + i * 16 + 4 * q + e;
-        if (m < M) store_output(E, m, ti.out_row0 + nloc, acc[i][j][e]);
-      }
     }
   }
 }
