@@ -34,6 +34,10 @@ LAYOUTS = [
     ("s1_k4096_u16_scale128", 384, 256, 8, 1, 4096, torch.uint16, None, {"scale_run": 128}),
     ("s1_k256_scale16_ragged_groups", 200, 384, 8, 1, 256, None, 96, {"scale_run": 16}),
     ("s3_groups256_ragged", 600, 384, 8, 3, 256, None, 256, {}),
+    # decode launches carry up to 4 groups in their kernel arguments; more
+    # groups are read from the plan
+    ("s1_k4096_groups4_scale32", 256, 256, 8, 1, 4096, torch.uint16, 64, {"scale_run": 32}),
+    ("s2_groups5_ragged", 280, 256, 8, 2, 256, None, 64, {}),
     ("s4_u8", 96, 256, 8, 4, 256, None, None, {}),
     ("s2_stage_scales", 128, 256, 8, 2, 256, None, None, {"stage_scales": True}),
     ("s2_bf16_codebooks", 128, 256, 8, 2, 256, None, None, {"cb_dtype": torch.bfloat16}),

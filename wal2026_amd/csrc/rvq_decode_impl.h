@@ -13,8 +13,8 @@
 //     [64c + 16q, 64c + 16q + 16), q = l / 16: one 128-bit load per stage for
 //     8-bit ids, two for 16-bit ids.
 //   * Software pipeline: the index loads (and the lane's row-scale load) of
-//     the item PF slots ahead (decode_prefetch) are issued right after an
-//     item is consumed, as straight-line code into a fixed register ring, so
+//     the item PF slots ahead (decode_prefetch) are issued as an item is
+//     taken from the ring, before its compute, as straight-line code, so
 //     the only memory waits in the loop are the in-order ones for the slot
 //     being consumed.  Loads past the end of the range get an out-of-range
 //     buffer offset and read zeros without touching memory.  Per-tile
@@ -46,7 +46,8 @@ constexpr int kDecodeMaxThreads = kDecodeMaxWaves * 64;
 // benchmark shape (c2, c3, c5): one item ahead is fastest.  The loop is bound
 // by the LDS codeword gathers and the dequantisation arithmetic, not by HBM
 // latency, and every deeper ring slot adds straight-line code and prologue
-// loads (PF 4 -> 1: c3 +4 %, c5 +8 %, c2 +5 % tokens/s).
+// loads (PF 4 -> 1: c3 +4 %, c5 +8 %, c2 +5 % tokens/s; with the refill
+// issued before the compute, PF 2 -> 1: c3 +4 %, c5 +7 %).
 template <int S, typename IdT>
 constexpr int decode_prefetch() {
   return 1;
@@ -360,6 +361,16 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
         if constexpr (!SCALED) rs = make_row_scale<XDT>(scale_bits_to_f32(rsr[j], D.sc_dtype));
         acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       }
+      // Take this item's indices out of the ring and refill the slot with the
+      // item PF ahead (uniform) before computing, so that load's latency runs
+      // under this item's gathers and MFMAs (c3 +5 %, c5 +4 % tokens/s
+      // against a refill after the compute).
+      u32x4_t cur[S][NV];
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) cur[s][v] = ring[j][s][v];
+      if (i0 + j + PF < n_items) issue(j);
       const int c = wave + NW * ct_c;
       if (live && c < nchunk) {  // uniform across the wave
         const int base = c * 64 + 16 * q;
@@ -376,7 +387,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
         for (int tt = 0; tt < 16; ++tt) {
           uint32_t id[S];
 #pragma unroll
-          for (int s = 0; s < S; ++s) id[s] = extract_id<IdT>(ring[j][s], tt) & kmask;
+          for (int s = 0; s < S; ++s) id[s] = extract_id<IdT>(cur[s], tt) & kmask;
           if constexpr (SCALED) wf[tt] = *reinterpret_cast<const u32x4_t*>(tbl + (size_t)id[0] * 16);
           else wf[tt] = make_wfrag<S, LMODE, SEM, XDT>(tbl, id, K, L.active_mask, rs);
         }
@@ -396,7 +407,6 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
           acc = mfma16<XDT>(xf, wf[tt], acc);
         }
       }
-      if (i0 + j + PF < n_items) issue(j);  // refill this slot with the item PF ahead (uniform)
       if (live && ++ct_c == CPT) {
         // tile done: park this wave's partial (rows m < M) in LDS
         ct_c = 0;
