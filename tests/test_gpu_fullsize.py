@@ -71,10 +71,14 @@ def test_full_decode_parity_and_linearity(shape, m, gpu_device):
     assert rel_err(y1 + y2, y) <= 1e-5, name
 
 
-def test_full_prefill_parity_sampled_rows(gpu_device):
+@pytest.mark.parametrize("tile", ["auto", "short"])
+def test_full_prefill_parity_sampled_rows(tile, gpu_device, monkeypatch):
     """c4: S = 2, K = 256, 8-bit ids, bf16 x, M = 2048 through the prefill
-    kernel; 24 sampled rows of y against the oracle."""
-    print("[fullsize] prefill c4 gate 2048x14336x4096", flush=True)
+    kernel (the launcher's choice there is the 256-row x tile; "short" forces
+    the 128-row one); 28 sampled rows of y against the oracle."""
+    if tile != "auto":
+        monkeypatch.setenv("WAL2026_PREFILL_TILE", tile)
+    print(f"[fullsize] prefill c4 gate 2048x14336x4096 tile={tile}", flush=True)
     cfg, mod, gen = _layer("c4", 14336, 4096, gpu_device)
     x = synth.make_activation(2048, 4096, cfg.x_dtype, gen)
     y = mod._hip_linear(x.to(gpu_device), fast=False, out_dtype=torch.float32).cpu()

@@ -34,8 +34,7 @@ LAYOUTS = [
     ("s1_k4096_u16_scale128", 384, 256, 8, 1, 4096, torch.uint16, None, {"scale_run": 128}),
     ("s1_k256_scale16_ragged_groups", 200, 384, 8, 1, 256, None, 96, {"scale_run": 16}),
     ("s3_groups256_ragged", 600, 384, 8, 3, 256, None, 256, {}),
-    # decode launches carry up to 4 groups in their kernel arguments; more
-    # groups are read from the plan
+    # four and five row groups in one launch
     ("s1_k4096_groups4_scale32", 256, 256, 8, 1, 4096, torch.uint16, 64, {"scale_run": 32}),
     ("s2_groups5_ragged", 280, 256, 8, 2, 256, None, 64, {}),
     ("s4_u8", 96, 256, 8, 4, 256, None, None, {}),
@@ -100,10 +99,33 @@ def test_linear_fp32_parity(layout, x_dtype, m, gpu_device):
     assert err <= 1e-5, f"{layout[0]} m={m}: {err:.3e} is above fp32 accumulation error"
 
 
-@pytest.mark.parametrize("layout", LAYOUTS[:9], ids=[l[0] for l in LAYOUTS[:9]])
+# The prefill launcher picks a 128- or 256-row x tile from the grid size;
+# WAL2026_PREFILL_TILE forces one (layouts with S > 2 or fp32 tables always
+# run the 128-row kernel).
+TILES = ["short", "tall"]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=[l[0] for l in LAYOUTS])
 @pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float16], ids=["xbf16", "xf16"])
-def test_onehot_prefill_tiles_bitexact(layout, x_dtype, gpu_device):
+@pytest.mark.parametrize("m", [17, 300])
+@pytest.mark.parametrize("tile", TILES)
+def test_prefill_tile_shapes_parity(layout, x_dtype, m, tile, gpu_device, monkeypatch):
+    monkeypatch.setenv("WAL2026_PREFILL_TILE", tile)
+    mod = _module(layout, gpu_device)
+    g = torch.Generator().manual_seed(m + 7)
+    x = torch.randn(m, mod.in_features, generator=g).to(x_dtype)
+    y = mod._hip_linear(x.to(gpu_device), fast=False, out_dtype=torch.float32)
+    w_ref = oracle_weight(module_buffers_as_encoding(mod), x_dtype)
+    err = rel_err(y, c_oracle.linear_f64(x, w_ref))
+    assert err <= 1e-5, f"{layout[0]} m={m} {tile}: max|dy|/max|y| = {err:.3e}"
+
+
+@pytest.mark.parametrize("layout", LAYOUTS[:11], ids=[l[0] for l in LAYOUTS[:11]])
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float16], ids=["xbf16", "xf16"])
+@pytest.mark.parametrize("tile", TILES)
+def test_onehot_prefill_tiles_bitexact(layout, x_dtype, tile, gpu_device, monkeypatch):
     """x = I (M = in_features > 16: prefill kernel) gives y = W^T exactly."""
+    monkeypatch.setenv("WAL2026_PREFILL_TILE", tile)
     mod = _module(layout, gpu_device)
     eye = torch.eye(mod.in_features, dtype=x_dtype, device=gpu_device)
     y = mod._hip_linear(eye, fast=False, out_dtype=torch.float32).cpu()

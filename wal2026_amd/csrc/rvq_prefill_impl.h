@@ -35,6 +35,9 @@
 // XCD keeps revisiting the same few x tiles in its L2.
 #pragma once
 
+#include <cstdlib>
+#include <cstring>
+
 #include "rvq_fragment.h"
 
 namespace wal {
@@ -261,6 +264,240 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tall tile: 256 x-rows x 256 weight rows, 12 waves.
+//
+// Each dequantised weight feeds BM MFMA rows, so doubling BM halves the
+// dequantisation work per flop.  Register budget: 12 waves are three per
+// SIMD, 168 registers per lane.
+//   * 8 consumer waves (two per SIMD), 2 (M) x 4 (N), each a 128 x 64 output
+//     tile: 128 accumulator registers; the step's four W fragments stay in
+//     registers and the eight x fragments are read one by one next to the
+//     MFMAs that use them.
+//   * 4 producer waves (one per SIMD); thread pt owns weight row pt (all 4
+//     blocks of a k-step) and copies 4 of the x tile's 1024 16-byte pieces.
+// LDS rows are 64 bytes (one k-step of 16-bit values) with the 16-byte chunk
+// c of row r stored at chunk c ^ ((r >> 1) & 3): a fragment read (lane l:
+// row l % 16, chunk l / 16) is then conflict-free, as with a 96-byte stride,
+// in two thirds of the space.
+// ---------------------------------------------------------------------------
+constexpr int kTallConsumerWaves = 8;
+constexpr int kTallProducerWaves = 4;
+constexpr int kTallThreads = (kTallConsumerWaves + kTallProducerWaves) * 64;
+constexpr int kTallProducerThreads = kTallProducerWaves * 64;
+constexpr int TBM = 256;                  // x rows per workgroup tile
+constexpr int kTallRowBytes = PBK * 2;    // 64
+constexpr int kTallTileBytes = 256 * kTallRowBytes;  // one 256-row operand tile (16 KB)
+
+WAL_HOST_DEVICE constexpr int tall_swz(int row, int chunk) { return (chunk ^ ((row >> 1) & 3)) * 16; }
+
+template <int S, typename IdT, int LMODE>
+WAL_HOST_DEVICE size_t prefill_tall_lds_bytes(int K, int rshift) {
+  return (size_t)4 * kTallTileBytes + ((size_t)prefill_table_entries<S, IdT>(K) * lds_entry_bytes<LMODE>() << rshift);
+}
+
+// Instances whose producer registers fit beside the pipeline (checked with
+// the compiler's resource report: no scratch).
+template <int S, typename IdT, int LMODE>
+constexpr bool tall_supported() {
+  return S <= 2 && LMODE != LM_F32;
+}
+
+template <int S, typename IdT, int LMODE, int SEM, int XDT>
+__global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
+                                                                        const uint16_t* __restrict__ x, int64_t M,
+                                                                        int n_mt, int rshift) {
+  constexpr int XP = TBM * 4 / kTallProducerThreads;  // 4 x pieces per producer thread per k-step
+  constexpr int NV = sizeof(IdT);
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* xs = smem;                          // [2][256 rows][64 B]
+  uint8_t* ws = smem + 2 * kTallTileBytes;     // [2][256 rows][64 B]
+  uint8_t* lds_cb = smem + 4 * kTallTileBytes;
+
+  const int K = L.codebook_size;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int mt = (int)(blockIdx.x % (unsigned)n_mt);
+  const int nt = (int)(blockIdx.x / (unsigned)n_mt);
+  const FragTile<S> ti = get_frag_tile<S>(L, nt);
+  const int64_t m0 = (int64_t)mt * TBM;
+  const int B = L.blocks_per_row;
+  const int in = L.in_features;
+  const int nk = B / 4;
+  const uint32_t kmax = (uint32_t)(K - 1);
+
+  constexpr int ESZ = lds_entry_bytes<LMODE>();
+  if (rshift == 0) {
+    stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, ti.p, K, D);
+  } else {
+    uint8_t* compact = ws;  // the W tiles are idle until the first step
+    stage_codebooks<S, LMODE, SEM, XDT>(compact, ti.p, K, D);
+    __syncthreads();
+    const int n16 = prefill_table_entries<S, IdT>(K) * (ESZ / 16);
+    const int nc = 1 << rshift;
+    for (int i = tid; i < n16 * nc; i += kTallThreads) {
+      const int piece = i >> rshift, c = i & (nc - 1);
+      const int e = piece / (ESZ / 16), h = piece - e * (ESZ / 16);
+      *reinterpret_cast<u32x4_t*>(lds_cb + (((e << rshift) + c) * ESZ) + 16 * h) =
+          *reinterpret_cast<const u32x4_t*>(compact + (size_t)piece * 16);
+    }
+  }
+  __syncthreads();
+
+  if (wave < kTallConsumerWaves) {
+    const int wm = wave >> 2, wn = wave & 3;
+    const int l16 = lane & 15, q = lane >> 4;
+    const int sw = tall_swz(l16, q);  // fragment rows start at multiples of 16
+    const uint8_t* xa = xs + (wm * 128 + l16) * kTallRowBytes + sw;
+    const uint8_t* wb = ws + (wn * 64 + l16) * kTallRowBytes + sw;
+    f32x4_t acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();  // step 0 produced
+    for (int k = 0; k < nk; ++k) {
+      const int bo = (k & 1) * kTallTileBytes;
+      u32x4_t b[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(wb + bo + j * 16 * kTallRowBytes);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa + bo + i * 16 * kTallRowBytes);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<XDT>(a, b[j], acc[i][j]);
+      }
+      __syncthreads();  // buffer k & 1 read; step k + 1 produced
+    }
+    // Epilogue through LDS (the operand tiles are idle after the last
+    // barrier): per 16-row slice the wave parks its 16 x 64 accumulators in
+    // a private 4 KB area and reads them back one output row per
+    // instruction.  The stores are coalesced, and acc is indexed by
+    // constants only (a loop over it would put the array in scratch memory).
+    float* stage = reinterpret_cast<float*>(smem) + wave * 16 * 64;
+    const int nloc = wn * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) stage[(4 * q + e) * 64 + j * 16 + l16] = acc[i][j][e];
+      // (one wave's LDS accesses run in order: the reads see these writes,
+      // and the next slice's writes wait for these reads)
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wm * 128 + i * 16 + r;
+        const float v = stage[r * 64 + lane];
+        if (m < M && nloc < ti.rows) store_output(E, m, ti.out_row0 + nloc, v);
+      }
+    }
+    return;
+  }
+
+  // ---- producers: thread pt owns weight row pt ----
+  const int pt = tid - kTallConsumerWaves * 64;
+  const uint8_t* lds_lane = lds_cb + (lane & ((1 << rshift) - 1)) * ESZ;
+  const int64_t wr = ti.row0 + (pt < ti.rows ? pt : 0);  // rows past the tile: never stored
+  const RowScale rs = make_row_scale<XDT>(load_f(ti.p.row_scale, D.sc_dtype, scale_index(L, wr)));
+  bufrsrc_t idr[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) idr[s] = make_rsrc(ti.p.ids[s]);
+  const uint32_t idrow = (uint32_t)(wr * B * (int64_t)sizeof(IdT));
+  // x pieces p = pt + i * 256: row p / 4, 16-byte chunk p % 4
+  const bufrsrc_t xr = make_rsrc(x + m0 * in);
+  uint32_t xoff[XP];
+  int xdst[XP];
+#pragma unroll
+  for (int i = 0; i < XP; ++i) {
+    const int p = pt + i * kTallProducerThreads;
+    const int r = p >> 2, c = p & 3;
+    xoff[i] = m0 + r < M ? (uint32_t)((r * in + 8 * c) * 2) : kBufOOB;
+    xdst[i] = r * kTallRowBytes + tall_swz(r, c);
+  }
+  uint8_t* wd = ws + pt * kTallRowBytes;
+  auto load_x = [&](int k, u32x4_t (&dst)[XP]) {
+    const uint32_t step = k < nk ? (uint32_t)(k * PBK * 2) : kBufOOB;
+#pragma unroll
+    for (int i = 0; i < XP; ++i) dst[i] = ldbuf128(xr, xoff[i] == kBufOOB ? kBufOOB : xoff[i] + step);
+  };
+  auto load_ids = [&](int grp, u32x4_t (&dst)[S][NV]) {
+    const uint32_t off = grp * 4 < nk ? idrow + (uint32_t)(grp * 16 * NV) : kBufOOB;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int v = 0; v < NV; ++v) dst[s][v] = ldbuf128(idr[s], off == kBufOOB ? kBufOOB : off + 16 * v);
+  };
+  auto produce = [&](int k, int buf, const u32x4_t (&ids)[S][NV], const u32x4_t (&xv)[XP]) {
+    WfragRaw<S, LMODE> raw[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int t = 4 * (k & 3) + b;  // block inside the 16-block index group
+      uint32_t id[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        if constexpr (NV == 1) {
+          id[s] = (ids[s][0][t >> 2] >> (8 * (t & 3))) & 0xffu;  // inside the allocation
+        } else {
+          id[s] = min((ids[s][t >> 3][(t >> 1) & 3] >> (16 * (t & 1))) & 0xffffu, kmax);
+        }
+      }
+      raw[b] = gather_wfrag_rep<S, LMODE>(lds_lane, id, K, rshift);
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      *reinterpret_cast<u32x4_t*>(wd + buf * kTallTileBytes + tall_swz(pt, b)) =
+          combine_wfrag<S, LMODE, SEM, XDT>(raw[b], L.active_mask, rs);
+#pragma unroll
+    for (int i = 0; i < XP; ++i) *reinterpret_cast<u32x4_t*>(xs + buf * kTallTileBytes + xdst[i]) = xv[i];
+  };
+
+  u32x4_t xq[4][XP];      // x pieces of steps k + 1 .. k + 4 (slot = step & 3)
+  u32x4_t idq[2][S][NV];  // index bytes of two groups of 4 k-steps (slot = group & 1)
+  load_ids(0, idq[0]);
+  load_ids(1, idq[1]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) load_x(j, xq[j]);
+  produce(0, 0, idq[0], xq[0]);
+  load_x(4, xq[0]);
+  __syncthreads();  // step 0 produced
+  for (int k0 = 0; k0 < nk; k0 += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      if (k >= nk) break;  // uniform
+      const int gs = ((u + 1) >> 2) & 1;
+      produce(k + 1, (u + 1) & 1, idq[gs], xq[(u + 1) & 3]);
+      load_x(k + 5, xq[(u + 1) & 3]);
+      if (((u + 1) & 3) == 3) load_ids(((k + 1) >> 2) + 2, idq[gs]);
+      __syncthreads();
+    }
+  }
+}
+
+template <int S, typename IdT, int LMODE, int SEM, int XDT>
+static hipError_t prefill_tall(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
+                               int64_t M, hipStream_t st) {
+  const size_t tbl = (size_t)prefill_table_entries<S, IdT>(L.codebook_size) * lds_entry_bytes<LMODE>();
+  int rshift = 3;
+  while (rshift > 0 && (prefill_tall_lds_bytes<S, IdT, LMODE>(L.codebook_size, rshift) > (size_t)160 * 1024 ||
+                        tbl > (size_t)2 * kTallTileBytes))
+    --rshift;
+  const size_t lds = prefill_tall_lds_bytes<S, IdT, LMODE>(L.codebook_size, rshift);
+  auto kern = rvq_prefill_tall_kernel<S, IdT, LMODE, SEM, XDT>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int n_mt = (int)((M + TBM - 1) / TBM);
+  dim3 grid((unsigned)(L.n_tiles * (int64_t)n_mt));
+  hipLaunchKernelGGL(kern, grid, dim3(kTallThreads), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M, n_mt,
+                     rshift);
+  return hipGetLastError();
+}
+
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int TM>
 static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
                              int64_t M, hipStream_t st) {
@@ -294,7 +531,25 @@ static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const Epilo
 template <int S, typename IdT, int LMODE, int SEM, int XDT>
 static hipError_t prefill_go(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
                              int64_t M, int n_cu, hipStream_t st) {
-  (void)n_cu;
+  if constexpr (tall_supported<S, IdT, LMODE>()) {
+    // WAL2026_PREFILL_TILE=tall|short forces a tile shape (tests, tuning).
+    const char* force = getenv("WAL2026_PREFILL_TILE");
+    bool tall;
+    if (force != nullptr && strcmp(force, "tall") == 0) {
+      tall = true;
+    } else if (force != nullptr && strcmp(force, "short") == 0) {
+      tall = false;
+    } else {
+      // One workgroup per CU: compare the rounds of workgroups each shape
+      // needs, a tall workgroup costing kTallCost / 8 of a short one's two.
+      constexpr int64_t kTallCost = 10;
+      const int64_t cu = n_cu > 0 ? n_cu : 256;
+      const int64_t r_short = (L.n_tiles * ((M + 127) / 128) + cu - 1) / cu;
+      const int64_t r_tall = (L.n_tiles * ((M + TBM - 1) / TBM) + cu - 1) / cu;
+      tall = r_tall * kTallCost <= r_short * 8;
+    }
+    if (tall) return prefill_tall<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
+  }
   return prefill_tm<S, IdT, LMODE, SEM, XDT, 4>(L, D, E, x, M, st);
 }
 
