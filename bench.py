@@ -278,7 +278,7 @@ def main() -> int:
         tflops = dom_flops / (dom_us * 1e-6) / 1e12
         roofline = {
             "bound": "mfma",
-            "kernel": f"rvq_prefill_kernel ({dom_name}, {dom_flops} flop)",
+            "kernel": f"rvq_prefill_tall/wide_kernel, launcher's choice ({dom_name}, {dom_flops} flop)",
             "achieved": round(tflops, 1),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",

@@ -71,11 +71,11 @@ def test_full_decode_parity_and_linearity(shape, m, gpu_device):
     assert rel_err(y1 + y2, y) <= 1e-5, name
 
 
-@pytest.mark.parametrize("tile", ["auto", "short"])
+@pytest.mark.parametrize("tile", ["auto", "short", "wide"])
 def test_full_prefill_parity_sampled_rows(tile, gpu_device, monkeypatch):
     """c4: S = 2, K = 256, 8-bit ids, bf16 x, M = 2048 through the prefill
-    kernel (the launcher's choice there is the 256-row x tile; "short" forces
-    the 128-row one); 28 sampled rows of y against the oracle."""
+    kernel, with the launcher's tile choice and with the 128 x 256 and 256 x
+    128 tiles forced; 28 sampled rows of y against the oracle."""
     if tile != "auto":
         monkeypatch.setenv("WAL2026_PREFILL_TILE", tile)
     print(f"[fullsize] prefill c4 gate 2048x14336x4096 tile={tile}", flush=True)

@@ -99,10 +99,10 @@ def test_linear_fp32_parity(layout, x_dtype, m, gpu_device):
     assert err <= 1e-5, f"{layout[0]} m={m}: {err:.3e} is above fp32 accumulation error"
 
 
-# The prefill launcher picks a 128- or 256-row x tile from the grid size;
-# WAL2026_PREFILL_TILE forces one (layouts with S > 2 or fp32 tables always
-# run the 128-row kernel).
-TILES = ["short", "tall"]
+# The prefill launcher picks its tile shape from the grid size;
+# WAL2026_PREFILL_TILE forces one: short = 128 x-rows x 256 weight rows,
+# tall = 256 x 256 (S <= 2, 16-bit tables), wide = 256 x 128.
+TILES = ["short", "tall", "wide"]
 
 
 @pytest.mark.parametrize("layout", LAYOUTS, ids=[l[0] for l in LAYOUTS])

@@ -35,6 +35,7 @@
 // XCD keeps revisiting the same few x tiles in its L2.
 #pragma once
 
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 
@@ -498,6 +499,224 @@ static hipError_t prefill_tall(const LayerArgs& L, const DtypeArgs& D, const Epi
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Wide tile: 256 x-rows x 128 weight rows, 16 waves (four per SIMD, 128
+// registers per lane).  Each dequantised weight feeds 256 MFMA rows, as in
+// the tall tile, and the two waves of each role per SIMD keep both the
+// matrix core and the VALU issuing (one wave alone issues VALU work at about
+// half the SIMD's rate).  The workgroup takes one half of a 256-row weight
+// tile (a half past the tile's rows exits at once).
+//   * 8 consumer waves, 4 (M) x 2 (N), each a 64 x 64 output tile.
+//   * 8 producer waves: thread pt dequantises block pt % 4 of weight row
+//     pt / 4 per k-step and copies 2 of the x tile's 1024 16-byte pieces.
+// LDS rows and swizzle as in the tall tile.
+// ---------------------------------------------------------------------------
+constexpr int kWideThreads = 1024;
+constexpr int kWideProducerThreads = 512;
+constexpr int WBN = 128;  // weight rows per workgroup
+constexpr int kWideXBytes = TBM * kTallRowBytes;  // 16 KB
+constexpr int kWideWBytes = WBN * kTallRowBytes;  // 8 KB
+
+template <int S, typename IdT, int LMODE>
+WAL_HOST_DEVICE size_t prefill_wide_lds_bytes(int K, int rshift) {
+  return (size_t)2 * (kWideXBytes + kWideWBytes) +
+         ((size_t)prefill_table_entries<S, IdT>(K) * lds_entry_bytes<LMODE>() << rshift);
+}
+
+// Instances that fit 128 registers per lane without scratch (compiler
+// resource report).
+template <int S, typename IdT, int LMODE>
+constexpr bool wide_supported() {
+  return !(S >= 4 && LMODE == LM_F32 && sizeof(IdT) == 2);
+}
+
+template <int S, typename IdT, int LMODE, int SEM, int XDT>
+__global__ __launch_bounds__(kWideThreads) void rvq_prefill_wide_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
+                                                                        const uint16_t* __restrict__ x, int64_t M,
+                                                                        int n_mt, int rshift) {
+  constexpr int XP = TBM * 4 / kWideProducerThreads;  // 2 x pieces per producer thread per k-step
+  constexpr int NV = sizeof(IdT);
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* xs = smem;                    // [2][256 rows][64 B]
+  uint8_t* ws = smem + 2 * kWideXBytes;  // [2][128 rows][64 B]
+  uint8_t* lds_cb = ws + 2 * kWideWBytes;
+
+  const int K = L.codebook_size;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int mt = (int)(blockIdx.x % (unsigned)n_mt);
+  const int nh = (int)(blockIdx.x / (unsigned)n_mt);
+  const FragTile<S> ti = get_frag_tile<S>(L, nh >> 1);
+  const int half = (nh & 1) * WBN;
+  const int rows_here = min(WBN, ti.rows - half);
+  if (rows_here <= 0) return;  // uniform: the whole workgroup
+  const int64_t m0 = (int64_t)mt * TBM;
+  const int B = L.blocks_per_row;
+  const int in = L.in_features;
+  const int nk = B / 4;
+  const uint32_t kmax = (uint32_t)(K - 1);
+
+  constexpr int ESZ = lds_entry_bytes<LMODE>();
+  if (rshift == 0) {
+    stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, ti.p, K, D);
+  } else {
+    uint8_t* compact = xs;  // the x tiles are idle until the first step
+    stage_codebooks<S, LMODE, SEM, XDT>(compact, ti.p, K, D);
+    __syncthreads();
+    const int n16 = prefill_table_entries<S, IdT>(K) * (ESZ / 16);
+    const int nc = 1 << rshift;
+    for (int i = tid; i < n16 * nc; i += kWideThreads) {
+      const int piece = i >> rshift, c = i & (nc - 1);
+      const int e = piece / (ESZ / 16), h = piece - e * (ESZ / 16);
+      *reinterpret_cast<u32x4_t*>(lds_cb + (((e << rshift) + c) * ESZ) + 16 * h) =
+          *reinterpret_cast<const u32x4_t*>(compact + (size_t)piece * 16);
+    }
+  }
+  __syncthreads();
+
+  if (wave < 8) {
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l16 = lane & 15, q = lane >> 4;
+    const int sw = tall_swz(l16, q);
+    const uint8_t* xa = xs + (wm * 64 + l16) * kTallRowBytes + sw;
+    const uint8_t* wb = ws + (wn * 64 + l16) * kTallRowBytes + sw;
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();  // step 0 produced
+    for (int k = 0; k < nk; ++k) {
+      const int bx = (k & 1) * kWideXBytes, bw = (k & 1) * kWideWBytes;
+      u32x4_t a[4], b[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(wb + bw + j * 16 * kTallRowBytes);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const u32x4_t*>(xa + bx + i * 16 * kTallRowBytes);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<XDT>(a[i], b[j], acc[i][j]);
+      __syncthreads();  // buffer k & 1 read; step k + 1 produced
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int nloc = wn * 64 + j * 16 + l16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t m = m0 + wm * 64 + i * 16 + 4 * q + e;
+          if (m < M && nloc < rows_here) store_output(E, m, ti.out_row0 + half + nloc, acc[i][j][e]);
+        }
+      }
+    }
+    return;
+  }
+
+  // ---- producers: thread pt dequantises block pt % 4 of row pt / 4 ----
+  const int pt = tid - 512;
+  const int prow = pt >> 2, pb = pt & 3;
+  const uint8_t* lds_lane = lds_cb + (lane & ((1 << rshift) - 1)) * ESZ;
+  const int64_t wr = ti.row0 + half + (prow < rows_here ? prow : 0);  // rows past the tile: never stored
+  const RowScale rs = make_row_scale<XDT>(load_f(ti.p.row_scale, D.sc_dtype, scale_index(L, wr)));
+  bufrsrc_t idr[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) idr[s] = make_rsrc(ti.p.ids[s]);
+  const uint32_t idrow = (uint32_t)(wr * B * (int64_t)sizeof(IdT));
+  const bufrsrc_t xr = make_rsrc(x + m0 * in);
+  uint32_t xoff[XP];
+  int xdst[XP];
+#pragma unroll
+  for (int i = 0; i < XP; ++i) {
+    const int p = pt + i * kWideProducerThreads;
+    const int r = p >> 2, c = p & 3;
+    xoff[i] = m0 + r < M ? (uint32_t)((r * in + 8 * c) * 2) : kBufOOB;
+    xdst[i] = r * kTallRowBytes + tall_swz(r, c);
+  }
+  uint8_t* wd = ws + prow * kTallRowBytes + tall_swz(prow, pb);
+  auto load_x = [&](int k, u32x4_t (&dst)[XP]) {
+    const uint32_t step = k < nk ? (uint32_t)(k * PBK * 2) : kBufOOB;
+#pragma unroll
+    for (int i = 0; i < XP; ++i) dst[i] = ldbuf128(xr, xoff[i] == kBufOOB ? kBufOOB : xoff[i] + step);
+  };
+  auto load_ids = [&](int grp, u32x4_t (&dst)[S][NV]) {
+    const uint32_t off = grp * 4 < nk ? idrow + (uint32_t)(grp * 16 * NV) : kBufOOB;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int v = 0; v < NV; ++v) dst[s][v] = ldbuf128(idr[s], off == kBufOOB ? kBufOOB : off + 16 * v);
+  };
+  auto produce = [&](int k, int buf, const u32x4_t (&ids)[S][NV], const u32x4_t (&xv)[XP]) {
+    // block 4 (k & 3) + pb of the 16-block index group; k & 3 is a constant
+    // of the unrolled loop, pb is not, so the vector words are picked with
+    // constant indices and a select (a register array indexed by a variable
+    // would be copied to scratch memory)
+    const int c = k & 3;
+    uint32_t id[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if constexpr (NV == 1) {
+        id[s] = (ids[s][0][c] >> (8 * pb)) & 0xffu;  // inside the allocation
+      } else {
+        const uint32_t lo = ids[s][c >> 1][(2 * c) & 3], hi = ids[s][c >> 1][(2 * c + 1) & 3];
+        id[s] = min(((pb & 2 ? hi : lo) >> (16 * (pb & 1))) & 0xffffu, kmax);
+      }
+    }
+    const WfragRaw<S, LMODE> raw = gather_wfrag_rep<S, LMODE>(lds_lane, id, K, rshift);
+#pragma unroll
+    for (int i = 0; i < XP; ++i) *reinterpret_cast<u32x4_t*>(xs + buf * kWideXBytes + xdst[i]) = xv[i];
+    *reinterpret_cast<u32x4_t*>(wd + buf * kWideWBytes) = combine_wfrag<S, LMODE, SEM, XDT>(raw, L.active_mask, rs);
+  };
+
+  u32x4_t xq[4][XP];
+  u32x4_t idq[2][S][NV];
+  load_ids(0, idq[0]);
+  load_ids(1, idq[1]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) load_x(j, xq[j]);
+  produce(0, 0, idq[0], xq[0]);
+  load_x(4, xq[0]);
+  __syncthreads();  // step 0 produced
+  for (int k0 = 0; k0 < nk; k0 += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      if (k >= nk) break;  // uniform
+      const int gs = ((u + 1) >> 2) & 1;
+      produce(k + 1, (u + 1) & 1, idq[gs], xq[(u + 1) & 3]);
+      load_x(k + 5, xq[(u + 1) & 3]);
+      if (((u + 1) & 3) == 3) load_ids(((k + 1) >> 2) + 2, idq[gs]);
+      __syncthreads();
+    }
+  }
+}
+
+template <int S, typename IdT, int LMODE, int SEM, int XDT>
+static hipError_t prefill_wide(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
+                               int64_t M, hipStream_t st) {
+  const size_t tbl = (size_t)prefill_table_entries<S, IdT>(L.codebook_size) * lds_entry_bytes<LMODE>();
+  int rshift = 3;
+  while (rshift > 0 && (prefill_wide_lds_bytes<S, IdT, LMODE>(L.codebook_size, rshift) > (size_t)160 * 1024 ||
+                        tbl > (size_t)2 * kWideXBytes))
+    --rshift;
+  const size_t lds = prefill_wide_lds_bytes<S, IdT, LMODE>(L.codebook_size, rshift);
+  auto kern = rvq_prefill_wide_kernel<S, IdT, LMODE, SEM, XDT>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int n_mt = (int)((M + TBM - 1) / TBM);
+  dim3 grid((unsigned)(L.n_tiles * (int64_t)2 * n_mt));
+  hipLaunchKernelGGL(kern, grid, dim3(kWideThreads), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M, n_mt,
+                     rshift);
+  return hipGetLastError();
+}
+
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int TM>
 static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
                              int64_t M, hipStream_t st) {
@@ -531,25 +750,31 @@ static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const Epilo
 template <int S, typename IdT, int LMODE, int SEM, int XDT>
 static hipError_t prefill_go(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
                              int64_t M, int n_cu, hipStream_t st) {
-  if constexpr (tall_supported<S, IdT, LMODE>()) {
-    // WAL2026_PREFILL_TILE=tall|short forces a tile shape (tests, tuning).
-    const char* force = getenv("WAL2026_PREFILL_TILE");
-    bool tall;
-    if (force != nullptr && strcmp(force, "tall") == 0) {
-      tall = true;
-    } else if (force != nullptr && strcmp(force, "short") == 0) {
-      tall = false;
-    } else {
-      // One workgroup per CU: compare the rounds of workgroups each shape
-      // needs, a tall workgroup costing kTallCost / 8 of a short one's two.
-      constexpr int64_t kTallCost = 10;
-      const int64_t cu = n_cu > 0 ? n_cu : 256;
-      const int64_t r_short = (L.n_tiles * ((M + 127) / 128) + cu - 1) / cu;
-      const int64_t r_tall = (L.n_tiles * ((M + TBM - 1) / TBM) + cu - 1) / cu;
-      tall = r_tall * kTallCost <= r_short * 8;
-    }
-    if (tall) return prefill_tall<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
+  // WAL2026_PREFILL_TILE=short|tall|wide forces a tile shape (tests, tuning).
+  const char* force = getenv("WAL2026_PREFILL_TILE");
+  constexpr bool can_tall = tall_supported<S, IdT, LMODE>(), can_wide = wide_supported<S, IdT, LMODE>();
+  int shape = 0;  // 0 short, 1 tall, 2 wide
+  if (force != nullptr && strcmp(force, "short") == 0) {
+    shape = 0;
+  } else if (force != nullptr && strcmp(force, "tall") == 0) {
+    shape = can_tall ? 1 : 0;
+  } else if (force != nullptr && strcmp(force, "wide") == 0) {
+    shape = can_wide ? 2 : 0;
+  } else if (M > 128) {
+    // One workgroup per CU, and every shape's workgroup runs the same k-steps:
+    // cost = rounds of workgroups x time per k-step, measured at c4 (gfx950)
+    // as 0.84 (short), 1.22 (tall), 0.76 (wide) us.
+    const int64_t cu = n_cu > 0 ? n_cu : 256;
+    const int64_t mt256 = (M + TBM - 1) / TBM;
+    const int64_t c_short = (L.n_tiles * ((M + 127) / 128) + cu - 1) / cu * 84;
+    const int64_t c_tall = can_tall ? (L.n_tiles * mt256 + cu - 1) / cu * 122 : INT64_MAX;
+    const int64_t c_wide = can_wide ? (L.n_tiles * 2 * mt256 + cu - 1) / cu * 76 : INT64_MAX;
+    shape = c_tall <= c_wide && c_tall < c_short ? 1 : (c_wide < c_short ? 2 : 0);
   }
+  if constexpr (can_tall)
+    if (shape == 1) return prefill_tall<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
+  if constexpr (can_wide)
+    if (shape == 2) return prefill_wide<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
   return prefill_tm<S, IdT, LMODE, SEM, XDT, 4>(L, D, E, x, M, st);
 }
 
