@@ -134,6 +134,11 @@ LayerArgs make_args(const wal_rvq_layer& L, int kind, uint32_t active_mask) {
   A.g0 = L.groups[0];
   A.n_groups = L.n_groups;
   A.image = nullptr;
+  if (A.plan != nullptr) {
+    const PlanLayout P = plan_layout(L);
+    A.plan_tiles = reinterpret_cast<const PlanTile*>(static_cast<const char*>(L.plan) + P.tiles_offset[kind]);
+    A.plan_groups = reinterpret_cast<const wal_rvq_group*>(static_cast<const char*>(L.plan) + P.groups_offset);
+  }
   return A;
 }
 

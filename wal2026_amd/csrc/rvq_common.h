@@ -110,6 +110,11 @@ struct LayerArgs {
   const uint8_t* image;    // codebook image (per group: S x K staged entries) or NULL
   int32_t n_groups;
   int32_t pad2;
+  // The plan's tile table for this launch's tile kind and its group table
+  // (NULL without a plan): a kernel reads them without first reading the
+  // plan header.
+  const PlanTile* plan_tiles;
+  const wal_rvq_group* plan_groups;
 };
 
 // row_scale entry of row r (inside its group): r / scale_rows, a shift when

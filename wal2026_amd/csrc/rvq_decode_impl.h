@@ -91,13 +91,10 @@ WAL_DEVICE FragTile<S> tile_at(const LayerArgs& L, int t) {
     f.out_row0 = L.g0.row0 + f.row0;
     f.grows = L.g0.rows;
   } else {
-    typedef const __attribute__((address_space(4))) PlanHeader c_header_t;
     typedef const __attribute__((address_space(4))) PlanTile c_tile_t;
     typedef const __attribute__((address_space(4))) wal_rvq_group c_group_t;
-    const __attribute__((address_space(4))) char* base = (const __attribute__((address_space(4))) char*)(L.plan);
-    c_header_t* H = (c_header_t*)base;
-    c_tile_t* pt = (c_tile_t*)(base + H->tiles_offset[0]) + t;
-    c_group_t* G = (c_group_t*)(base + H->groups_offset) + pt->group;
+    c_tile_t* pt = (c_tile_t*)(L.plan_tiles) + t;
+    c_group_t* G = (c_group_t*)(L.plan_groups) + pt->group;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       f.p.ids[s] = G->stage_ids[s];
@@ -158,7 +155,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   // Touch every cache line of the kernel arguments at once: otherwise the
   // compiler loads each field where it is first used, and every first touch
   // of a line is its own dependent scalar-memory round trip.
-  asm volatile("" ::"s"(L.in_features), "s"(L.plan), "s"(L.g0.stage_ids[0]), "s"(L.g0.codebooks[4]),
+  asm volatile("" ::"s"(L.in_features), "s"(L.plan_tiles), "s"(L.plan_groups), "s"(L.g0.stage_ids[0]), "s"(L.g0.codebooks[4]),
                "s"(L.g0.row_scale), "s"(L.image), "s"(D.x_dtype), "s"(E.y), "s"(E.bias_mode), "s"(x), "s"(nslots));
   constexpr bool XLDS = XMODE == XM_LDS || XMODE == XM_REG;
   constexpr bool XREG = XMODE == XM_REG || XMODE == XM_GREG;
@@ -205,13 +202,26 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   // loads are issued before the index ring, so waiting for them (vmcnt is
   // in order) does not wait for the cold index loads behind them.
   FragTile<S> cti = tile_at<S>(L, t_begin);
-  int seg1 = t_begin + (cti.grows - cti.row0 + 15) / 16;  // first tile of the next group
+  const int gseg = t_begin + (cti.grows - cti.row0 + 15) / 16;  // first tile of the next group
+  int seg1 = gseg;
   if constexpr (SCALED) {
     const int run_left = L.scale_rows - (cti.row0 & (L.scale_rows - 1));  // scale_rows: power of two >= 16
     seg1 = min(seg1, t_begin + run_left / 16);
   }
   const bool two = seg1 < t_end && nslots == 2;
-  FragTile<S> sti = two ? tile_at<S>(L, seg1) : cti;
+  FragTile<S> sti = cti;
+  if (two) {
+    if (seg1 < gseg) {
+      // a scale-run boundary inside the group: the group's tiles are
+      // consecutive 16-row tiles, so no table read is needed
+      const int dr = (seg1 - t_begin) * 16;
+      sti.row0 += dr;
+      sti.out_row0 += dr;
+      sti.rows = min(16, sti.grows - sti.row0);
+    } else {
+      sti = tile_at<S>(L, seg1);
+    }
+  }
   int key[2] = {table_key<S, SCALED>(L, cti), two ? table_key<S, SCALED>(L, sti) : -1};
   const bool have_image = L.image != nullptr;
   const uint8_t* img0 = have_image ? L.image + (size_t)cti.group * tbl_bytes : nullptr;
