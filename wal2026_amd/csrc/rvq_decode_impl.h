@@ -63,12 +63,14 @@ WAL_DEVICE uint32_t extract_id(const u32x4_t (&v)[sizeof(IdT)], int t) {
 }
 
 // Bytes of LDS a decode launch needs: nslots staged tables (the codebooks of
-// up to two groups / scale runs), the per-tile partial sums of every wave
-// (max_tiles tiles per workgroup), a 256-byte zero row and (xlds) the
-// activation rows.
+// up to two groups / scale runs), the per-tile partial sums of every wave and
+// the output rows of every tile (max_tiles tiles per workgroup), a 256-byte
+// zero row and (xlds) the activation rows.
+constexpr int kDecodeTileMetaBytes = 16;  // {out_row0, rows, -, -} per tile
 template <int LMODE>
 WAL_HOST_DEVICE size_t decode_lds_bytes(int S, int K, bool xlds, int M, int in, int nw, int max_tiles, int nslots) {
-  return (size_t)nslots * S * K * lds_entry_bytes<LMODE>() + (size_t)max_tiles * nw * M * 16 * sizeof(float) + 256 +
+  return (size_t)nslots * S * K * lds_entry_bytes<LMODE>() +
+         (size_t)max_tiles * (nw * M * 16 * sizeof(float) + kDecodeTileMetaBytes) + 256 +
          (xlds ? (size_t)M * in * sizeof(uint16_t) : 0);
 }
 
@@ -109,6 +111,23 @@ WAL_DEVICE FragTile<S> tile_at(const LayerArgs& L, int t) {
     f.grows = G->rows;
   }
   return f;
+}
+
+// Tile t + 1 from tile t (f).  A group's tiles are consecutive 16-row tiles
+// of the plan, so only the first tile of the next group is read from the
+// plan: inside the loop a plan read is a dependent scalar-memory round trip
+// (cold in L2 when the step streams more bytes than the caches hold) that
+// every wave of the workgroup would wait for.
+template <int S>
+WAL_DEVICE FragTile<S> next_tile(const LayerArgs& L, const FragTile<S>& f, int t_next) {
+  if (f.row0 + 16 < f.grows) {
+    FragTile<S> n = f;
+    n.row0 += 16;
+    n.out_row0 += 16;
+    n.rows = min(16, n.grows - n.row0);
+    return n;
+  }
+  return tile_at<S>(L, t_next);
 }
 
 // Staged-table key of a tile: its group, and for scaled tables its scale run.
@@ -171,7 +190,8 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   const int tbl_bytes = S * K * ESZ;  // one staged table (all stages of a group)
   uint8_t* lds_cb = smem;             // nslots (1 or 2) table slots
   float* part = reinterpret_cast<float*>(smem + (size_t)nslots * tbl_bytes);  // [max_tiles][NW][M * 16]
-  uint8_t* zrow = reinterpret_cast<uint8_t*>(part + (size_t)max_tiles * NW * M16);  // 256 zero bytes
+  int* tmeta = reinterpret_cast<int*>(part + (size_t)max_tiles * NW * M16);      // [max_tiles][4]
+  uint8_t* zrow = reinterpret_cast<uint8_t*>(tmeta + (size_t)max_tiles * 4);   // 256 zero bytes
   uint16_t* xs = reinterpret_cast<uint16_t*>(zrow + 256);                    // [M][in] when XLDS
 
   const int tid = threadIdx.x;
@@ -286,7 +306,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
     rsr[j] = ldbuf16(make_rsrc(iti.p.row_scale), is_t < n_tiles_wg ? (uint32_t)si * 2u : kBufOOB);
     if (++is_c == CPT) {
       is_c = 0;
-      if (++is_t < n_tiles_wg) iti = tile_at<S>(L, t_begin + is_t);
+      if (++is_t < n_tiles_wg) iti = next_tile<S>(L, iti, t_begin + is_t);
     }
   };
 #pragma unroll
@@ -349,7 +369,9 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
       const bool live = i0 + j < n_items;  // uniform
       if (live && ct_c == 0) {
         // first item of a tile: pick its table slot
-        cti = tile_at<S>(L, t_begin + ct_t);
+        if (ct_t > 0) cti = next_tile<S>(L, cti, t_begin + ct_t);  // tile t_begin: the prologue's
+        // the epilogue's output rows of this tile (no plan read there)
+        if (tid == 0) reinterpret_cast<int2*>(tmeta)[2 * ct_t] = make_int2(cti.out_row0, cti.rows);
         const int k = table_key<S, SCALED>(L, cti);
         if (k == key[0]) {
           slot = 0;
@@ -438,11 +460,11 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
     const int o = e - k * M16;
     const int m = o >> 4;
     const int nn = o & 15;
-    const FragTile<S> ft = tile_at<S>(L, t_begin + k);
+    const int2 orow = reinterpret_cast<const int2*>(tmeta)[2 * k];  // {first output row, rows}
     const float* pp = part + (size_t)k * NW * M16 + o;
     float v = 0.0f;
     for (int w = 0; w < NW; ++w) v += pp[w * M16];
-    if (nn < ft.rows) store_output(E, m, ft.out_row0 + nn, v);
+    if (nn < orow.y) store_output(E, m, orow.x + nn, v);
   }
 }
 
@@ -457,7 +479,7 @@ static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const Epilog
   // until it does.
   auto plan_for = [&](int nslots, bool xlds, int* grid, int* share) -> bool {
     const size_t fixed = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, 0, nslots);
-    const size_t per_tile = (size_t)nw * M * 16 * sizeof(float);
+    const size_t per_tile = (size_t)nw * M * 16 * sizeof(float) + kDecodeTileMetaBytes;
     if (fixed + per_tile > (size_t)kLdsMax) return false;
     const int fit = (int)(((size_t)kLdsMax - fixed) / per_tile);
     int g = n_cu < L.n_tiles ? n_cu : L.n_tiles;
