@@ -208,6 +208,19 @@ int wal_id_route_reconstruct(const void* ids, int id_dtype, int64_t n, int64_t k
                              const void* row_scale, int mode, int out_dtype, void* w_out,
                              void* stream);
 
+/* ---- encoder ------------------------------------------------------------- */
+
+/* Nearest codeword of every block: replaces _assign_to_codebook
+ * (src/block_vq.py:180-196), the assignment step of the reference's k-means
+ * encoder (_fit_kmeans :199-227, encode_block_residual_vq).
+ * blocks [n, d] and codebook [k_cb, d] fp32 row-major, d in {1, 2, 4, 8, 16,
+ * 32}, blocks 16-byte aligned when d % 4 == 0.  Writes ids [n] (int64) and
+ * min_dist [n] (fp32) with dist = (|b|^2 + |c|^2) - 2 b.c (:192), the sums and
+ * the dot product accumulated with fused multiply-adds in element order, and
+ * the first minimal codeword on ties (torch.min, :193).  Finite inputs. */
+int wal_rvq_assign(const float* blocks, int64_t n, int d, const float* codebook, int64_t k_cb,
+                   int64_t* ids, float* min_dist, void* stream);
+
 /* ---- misc ---------------------------------------------------------------- */
 
 /* Message for the last error on this thread ("" if none). */

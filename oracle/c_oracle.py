@@ -89,6 +89,9 @@ def lib() -> ctypes.CDLL:
         L.or_id_route_weight.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                          ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        L.or_assign.restype = None
+        L.or_assign.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                ctypes.c_void_p, ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -223,3 +226,14 @@ def id_route_weight(ids, codebook_sum, row_scale, *, mode: int, x_dtype: torch.d
     lib().or_id_route_weight(ids.data_ptr(), _ID_TAG[ids.dtype], n, k, cs.data_ptr(), _FLOAT_TAG[cs.dtype],
                              rs.data_ptr(), _FLOAT_TAG[rs.dtype], mode, _FLOAT_TAG[x_dtype], out.data_ptr())
     return out
+
+
+def assign(blocks: torch.Tensor, codebook: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Nearest codeword of every block (or_assign; reference src/block_vq.py:180-196)."""
+    b = _cpu(blocks).to(torch.float32).contiguous()
+    c = _cpu(codebook).to(torch.float32).contiguous()
+    n, d = b.shape
+    ids = torch.empty(n, dtype=torch.int64)
+    dist = torch.empty(n, dtype=torch.float32)
+    lib().or_assign(b.data_ptr(), n, d, c.data_ptr(), c.shape[0], ids.data_ptr(), dist.data_ptr())
+    return ids, dist

@@ -289,3 +289,32 @@ void or_id_route_weight(const void* ids, int id_dtype, int64_t n_rows, int64_t k
     }
   }
 }
+
+/* _assign_to_codebook, src/block_vq.py:180-196 (see rvq_oracle.h). */
+static float or_sq_norm(const float* v, int d) {
+  float s = v[0] * v[0];
+  for (int j = 1; j < d; ++j) s = fmaf(v[j], v[j], s);
+  return s;
+}
+
+void or_assign(const float* blocks, int64_t n, int d, const float* codebook, int64_t k_cb,
+               int64_t* ids, float* min_dist) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float* b = blocks + i * d;
+    const float bsq = or_sq_norm(b, d);
+    int64_t best = 0;
+    float best_d = INFINITY;
+    for (int64_t k = 0; k < k_cb; ++k) {
+      const float* c = codebook + k * d;
+      float dot = b[0] * c[0];
+      for (int j = 1; j < d; ++j) dot = fmaf(b[j], c[j], dot);
+      const float dist = (bsq + or_sq_norm(c, d)) - 2.0f * dot;
+      if (dist < best_d) {
+        best = k;
+        best_d = dist;
+      }
+    }
+    ids[i] = best;
+    min_dist[i] = best_d;
+  }
+}

@@ -107,6 +107,20 @@ void or_id_route_weight(const void* ids, int id_dtype, int64_t n_rows, int64_t k
                         const void* row_scale, int rs_dtype,
                         int mode, int x_dtype, uint16_t* w_out);
 
+/* _assign_to_codebook (src/block_vq.py:180-196): nearest codeword of every
+ * block, fp32 throughout.
+ *   code_sq[k] = sum_j c[k][j]^2, chunk_sq[i] = sum_j b[i][j]^2 and
+ *   dot[i][k] = sum_j b[i][j] * c[k][j]: first product, then fused
+ *   multiply-adds for j = 1..d-1 in order (as BLAS sgemm kernels accumulate);
+ *   dist[i][k] = (chunk_sq[i] + code_sq[k]) - 2 * dot[i][k]   (:192);
+ *   ids[i] = the first k of minimal dist[i][k] (strict <, from +inf:
+ *   torch.min's tie rule, :193), min_dist[i] = that distance.
+ * The reference leaves the order of its two sums and of the matmul to torch
+ * (oneDNN/BLAS); the order above is this build's canonical one, and the HIP
+ * kernel follows it exactly.  Finite inputs only. */
+void or_assign(const float* blocks, int64_t n, int d, const float* codebook, int64_t k_cb,
+               int64_t* ids, float* min_dist);
+
 #ifdef __cplusplus
 }
 #endif

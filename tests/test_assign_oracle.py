@@ -1,0 +1,92 @@
+"""Oracle pinning for the encoder's assignment step (CPU only).
+
+``or_assign`` restates ``_assign_to_codebook`` (reference src/block_vq.py:180-196).
+The reference ships no test or fixture for it, so it is pinned by what the
+mathematics fixes: the chosen codeword is the nearest one of a float64 brute
+force up to fp32 rounding, exact matches have distance exactly 0, ties go to
+the first index, and the reference's own torch expression picks the same
+codewords wherever the two nearest are not within rounding of each other.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import c_oracle
+
+D_VALUES = [1, 2, 4, 8, 16, 32]
+
+
+def _data(n, d, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(n, d, generator=g), torch.randn(k, d, generator=g) * 0.7
+
+
+def _exact(b, c):
+    return ((b.double()[:, None, :] - c.double()[None, :, :]) ** 2).sum(-1)
+
+
+def _bound(b, c):
+    # |fp32 dist - exact| <= (d + 3) ulp-scaled by the magnitudes involved
+    d = b.shape[1]
+    mag = (b.double() ** 2).sum(1)[:, None] + (c.double() ** 2).sum(1)[None, :] + \
+        2.0 * (b.double().abs() @ c.double().abs().t())
+    return (d + 4) * 2.0 ** -24 * mag
+
+
+@pytest.mark.parametrize("d", D_VALUES)
+@pytest.mark.parametrize("k", [1, 17, 256])
+def test_nearest_up_to_rounding(d, k):
+    b, c = _data(700, d, k, seed=d * 1000 + k)
+    ids, dist = c_oracle.assign(b, c)
+    ex = _exact(b, c)
+    bound = _bound(b, c)
+    rows = torch.arange(b.shape[0])
+    chosen = ex[rows, ids]
+    assert torch.all(chosen - ex.min(1).values <= 2 * bound[rows, ids] + 1e-30)
+    assert torch.all((dist.double() - chosen).abs() <= bound[rows, ids] + 1e-30)
+    if k == 1:
+        assert torch.all(ids == 0)
+
+
+def test_exact_match_has_zero_distance_and_ties_go_first():
+    b, c = _data(64, 8, 32, seed=3)
+    c[20] = c[7]            # duplicate codeword: the first copy wins
+    b[:10] = c[7]           # blocks equal to a codeword
+    ids, dist = c_oracle.assign(b, c)
+    assert torch.all(ids[:10] == 7)
+    assert torch.all(dist[:10] == 0.0)
+    assert not torch.any(ids == 20)
+
+
+def test_agrees_with_reference_expression():
+    """The reference's torch expression (src/block_vq.py:188-193), evaluated
+    here on the CPU: same codeword except where the two nearest distances are
+    within rounding of each other."""
+    b, c = _data(4000, 8, 256, seed=11)
+    ref = ((b * b).sum(1, keepdim=True) + (c * c).sum(1)[None, :] - 2.0 * (b @ c.t())).min(1).indices
+    ids, _ = c_oracle.assign(b, c)
+    diff = torch.nonzero(ids != ref).flatten()
+    assert diff.numel() <= 4
+    ex = _exact(b[diff], c)
+    bound = _bound(b[diff], c)
+    r = torch.arange(diff.numel())
+    assert torch.all((ex[r, ids[diff]] - ex[r, ref[diff]]).abs() <= 2 * (bound[r, ids[diff]] + bound[r, ref[diff]]))
+
+
+def test_planted_sign_error_is_caught():
+    """A plausible slip (+2 b.c instead of -2 b.c) fails the brute-force check."""
+    b, c = _data(300, 8, 64, seed=5)
+    wrong = ((b * b).sum(1, keepdim=True) + (c * c).sum(1)[None, :] + 2.0 * (b @ c.t())).min(1).indices
+    ex = _exact(b, c)
+    rows = torch.arange(b.shape[0])
+    assert torch.any(ex[rows, wrong] - ex.min(1).values > 1e-3)
+
+
+def test_assign_wrapper_validates_like_the_reference():
+    from wal2026_amd.block_vq import _assign_to_codebook
+
+    with pytest.raises(ValueError, match="non-empty"):
+        _assign_to_codebook(torch.empty(0, 8), torch.zeros(4, 8))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        _assign_to_codebook(torch.zeros(4, 8), torch.zeros(4, 8))

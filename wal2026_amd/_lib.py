@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "wal_rvq_group_linear_matmul",
     "wal_id_route_linear",
     "wal_id_route_reconstruct",
+    "wal_rvq_assign",
     "wal_last_error",
     "wal_abi_version",
 )
@@ -123,6 +124,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wal_id_route_linear.argtypes = [vp, i64, i64, i32, vp, i32, i64, vp, i64, i32, vp, vp, i32, i32, vp, i32, vp]
     L.wal_id_route_reconstruct.restype = i32
     L.wal_id_route_reconstruct.argtypes = [vp, i32, i64, i64, vp, i64, i32, vp, i32, i32, vp, vp]
+    L.wal_rvq_assign.restype = i32
+    L.wal_rvq_assign.argtypes = [vp, i64, i32, vp, i64, vp, vp, vp]
 
 
 def lib() -> ctypes.CDLL:

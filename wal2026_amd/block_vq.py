@@ -183,6 +183,38 @@ def _nearest(blocks: Tensor, codebook: Tensor, batch_size: int) -> tuple[Tensor,
     return ids, dist
 
 
+def _assign_to_codebook(blocks: Tensor, codebook: Tensor, batch_size: int = 16_384) -> tuple[Tensor, Tensor]:
+    """Nearest codeword of every block: ``(ids int64, min_dist float32)``.
+
+    Drop-in for the reference's ``_assign_to_codebook`` (src/block_vq.py:180-196),
+    computed by one HIP kernel (``wal_rvq_assign``) on the blocks' ROCm device:
+    ``dist = (|b|^2 + |c|^2) - 2 b.c`` in fp32, the sums and the dot product
+    accumulated with fused multiply-adds in element order, the first minimal
+    codeword on ties.  ``batch_size`` only bounded the reference's temporaries
+    and is accepted and ignored.  Block sizes 1, 2, 4, 8, 16 and 32; finite
+    inputs.  CPU tensors raise (the kernel is the only implementation).
+    """
+    del batch_size
+    if blocks.numel() == 0:
+        raise ValueError("blocks must be non-empty")
+    if blocks.ndim != 2 or codebook.ndim != 2 or blocks.shape[1] != codebook.shape[1]:
+        raise ValueError(f"expected blocks [n, d] and codebook [k, d], got {tuple(blocks.shape)} and "
+                         f"{tuple(codebook.shape)}")
+    from . import _lib
+
+    dev = _lib.require_rocm(blocks)
+    b = blocks.to(torch.float32).contiguous()
+    if b.data_ptr() % 16:
+        b = b.clone()
+    cb = codebook.to(device=dev, dtype=torch.float32).contiguous()
+    n, d = b.shape
+    ids = torch.empty(n, dtype=torch.int64, device=dev)
+    dist = torch.empty(n, dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().wal_rvq_assign(b.data_ptr(), n, d, cb.data_ptr(), cb.shape[0], ids.data_ptr(),
+                                         dist.data_ptr(), _lib.stream_ptr(dev)))
+    return ids, dist
+
+
 def _kmeans(sample: Tensor, k: int, iters: int, batch_size: int) -> Tensor:
     """Lloyd iterations from a seeded random subset; empty clusters are
     reseeded from random samples."""
@@ -193,7 +225,9 @@ def _kmeans(sample: Tensor, k: int, iters: int, batch_size: int) -> Tensor:
     gen.manual_seed(0)
     cb = sample[torch.randperm(sample.shape[0], generator=gen, device=sample.device)[:k]].clone()
     for _ in range(iters):
-        ids, _ = _nearest(sample, cb, batch_size)
+        # on a ROCm device the assignment is the HIP kernel; a CPU sample (the
+        # encoder runs offline) takes the torch expression of the same formula
+        ids, _ = _assign_to_codebook(sample, cb) if sample.is_cuda else _nearest(sample, cb, batch_size)
         counts = torch.bincount(ids, minlength=k)
         sums = torch.zeros_like(cb).index_add_(0, ids, sample)
         filled = counts > 0

@@ -492,4 +492,19 @@ int wal_id_route_reconstruct(const void* ids, int id_dtype, int64_t n, int64_t k
   return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_id_route_reconstruct launch");
 }
 
+int wal_rvq_assign(const float* blocks, int64_t n, int d, const float* codebook, int64_t k_cb, int64_t* ids,
+                   float* min_dist, void* stream) {
+  g_err[0] = 0;
+  if (n < 0) return fail(WAL_EINVAL, "n must be >= 0 (got %lld)", (long long)n);
+  if (n == 0) return WAL_OK;
+  if (!blocks || !codebook || !ids || !min_dist) return fail(WAL_EINVAL, "NULL buffer");
+  if (!(d == 1 || d == 2 || d == 4 || d == 8 || d == 16 || d == 32))
+    return fail(WAL_EUNSUPPORTED, "block size %d not supported (1, 2, 4, 8, 16 or 32)", d);
+  if (k_cb < 1 || k_cb > 0x7fffffff) return fail(WAL_EINVAL, "codebook size must be in [1, 2^31) (got %lld)", (long long)k_cb);
+  if (d % 4 == 0 && (reinterpret_cast<uintptr_t>(blocks) & 15u) != 0)
+    return fail(WAL_EINVAL, "blocks must be 16-byte aligned");
+  hipError_t e = launch_assign(blocks, n, d, codebook, (int)k_cb, ids, min_dist, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_assign launch");
+}
+
 }  // extern "C"

@@ -94,6 +94,11 @@ extern template hipError_t prefill_entry<WAL_F16, uint8_t>(const LayerArgs&, con
 extern template hipError_t prefill_entry<WAL_F16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
                                                             int, int, const void*, int64_t, int, hipStream_t);
 
+// Nearest codeword of n blocks of d floats (d in {1, 2, 4, 8, 16, 32}),
+// rvq_assign.hip.
+hipError_t launch_assign(const float* blocks, int64_t n, int d, const float* codebook, int K, int64_t* ids,
+                         float* min_dist, hipStream_t st);
+
 inline hipError_t launch_decode(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
                                 int lds_mode, const void* x, int M, int n_cu, hipStream_t st) {
   if (L.n_tiles == 0) return hipSuccess;
