@@ -150,6 +150,61 @@ def cpu_baseline(cfg: synth.Config, budget_s: float = 20.0) -> dict:
     }
 
 
+FP32_PEAK_TFLOPS = 157.3      # MI355X fp32
+
+
+def bench_encoder(args) -> int:
+    """The encoder's assignment step at c3 shapes: every 8-wide block of a
+    14336 x 4096 weight (7,340,032 blocks) against a 4096-entry codebook, as
+    the reference's encoder assigns all blocks after fitting
+    (src/block_vq.py:180-196).  value = blocks per second; the roofline is the
+    fp32 one over the distance flops 2 * n * K * d."""
+    from wal2026_amd.block_vq import _assign_to_codebook
+
+    dev = torch.device("cuda", 0)
+    n, d, k = 14336 * 4096 // 8, 8, 4096
+    gen = synth.generator(0, dev)
+    blocks = torch.randn(n, d, generator=gen, device=dev) * 0.02
+    cb = torch.randn(k, d, generator=gen, device=dev) * 0.02
+    for _ in range(args.warmup):
+        _assign_to_codebook(blocks, cb)
+    stream = torch.cuda.current_stream()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(args.steps):
+        _assign_to_codebook(blocks, cb)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    flops = 2.0 * n * k * d
+    out = {
+        "metric": "encoder assignment (nearest of 4096 codewords, d=8) blocks/s", "value": round(n / (ms * 1e-3), 1),
+        "unit": "blocks/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0, 0.02) blocks and codebook)",
+        "config": {"workload": "c3 gate_proj encode: 7,340,032 blocks of 8 against K=4096", "n_blocks": n, "k": k,
+                   "d": d},
+        "roofline": {"bound": "valu", "kernel": "rvq_assign_kernel<8, 4>",
+                     "achieved": round(flops / (ms * 1e-3) / 1e12, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(flops / (ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import c_oracle
+
+        sample = 8192
+        hb, hc = blocks[:sample].cpu(), cb.cpu()
+        t0 = time.perf_counter()
+        c_oracle.assign(hb, hc)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(sample / dt, 1), "unit": "blocks/s", "cores": 1, "kind": "port",
+                               "sample": f"{sample} of the {n} blocks through oracle or_assign (one thread), "
+                                         f"{dt:.2f} s"}
+    print(json.dumps(out))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,6 +220,8 @@ def main() -> int:
     ap.add_argument("--pmc-summary", default=None,
                     help="rocprofv3 --pmc summary giving the dominant kernel's HBM traffic (default: "
                          "profiles/<decode|prefill>_<config>_<launch>_pmc.txt when it exists)")
+    ap.add_argument("--encoder", action="store_true",
+                    help="time the encoder's assignment step (wal_rvq_assign) on c3's gate_proj blocks instead")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (the path has no multi-GPU code); "
@@ -173,6 +230,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         return 1
+
+    if args.encoder:
+        return bench_encoder(args)
 
     cfg = synth.CONFIGS[args.config]
     if args.m is not None and args.m != cfg.m:
