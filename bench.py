@@ -208,7 +208,8 @@ def bench_encoder(args) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 50; 128 for c5, the step count its survey figure is quoted over)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--m", type=int, default=None, help="activation rows (default: the config's, 1 for c3)")
@@ -223,6 +224,8 @@ def main() -> int:
     ap.add_argument("--encoder", action="store_true",
                     help="time the encoder's assignment step (wal_rvq_assign) on c3's gate_proj blocks instead")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 128 if args.config == "c5" and not args.encoder else 50
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (the path has no multi-GPU code); "
               "run with --gpus 1", file=sys.stderr)
