@@ -221,6 +221,17 @@ int wal_id_route_reconstruct(const void* ids, int id_dtype, int64_t n, int64_t k
 int wal_rvq_assign(const float* blocks, int64_t n, int d, const float* codebook, int64_t k_cb,
                    int64_t* ids, float* min_dist, void* stream);
 
+/* The reductions of the k-means centroid update in _fit_kmeans
+ * (src/block_vq.py:216-218): counts = bincount(ids, minlength=k_cb) and
+ * sums = zeros(k_cb, d).index_add_(0, ids, blocks), each sum taken in fp32
+ * from +0 in ascending block order (torch's CPU index_add_ order), so the
+ * results are deterministic.  ids [n] int64 in [0, k_cb) (ids outside that
+ * range are not counted: the caller checks them), blocks [n, d] fp32,
+ * d in {1, 2, 4, 8, 16, 32}; writes sums [k_cb, d] fp32 and counts [k_cb]
+ * int64 (zeros when n = 0). */
+int wal_rvq_centroid_sums(const int64_t* ids, int64_t n, const float* blocks, int d, int64_t k_cb,
+                          float* sums, int64_t* counts, void* stream);
+
 /* ---- misc ---------------------------------------------------------------- */
 
 /* Message for the last error on this thread ("" if none). */

@@ -89,6 +89,9 @@ def lib() -> ctypes.CDLL:
         L.or_id_route_weight.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                          ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        L.or_centroid_sums.restype = ctypes.c_int
+        L.or_centroid_sums.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_int64,
+                                       ctypes.c_void_p, ctypes.c_void_p]
         L.or_assign.restype = None
         L.or_assign.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
                                 ctypes.c_void_p, ctypes.c_void_p]
@@ -237,3 +240,16 @@ def assign(blocks: torch.Tensor, codebook: torch.Tensor) -> tuple[torch.Tensor, 
     dist = torch.empty(n, dtype=torch.float32)
     lib().or_assign(b.data_ptr(), n, d, c.data_ptr(), c.shape[0], ids.data_ptr(), dist.data_ptr())
     return ids, dist
+
+
+def centroid_sums(ids: torch.Tensor, blocks: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(sums [k, d] fp32, counts [k] int64) of the k-means update (or_centroid_sums;
+    reference src/block_vq.py:216-218)."""
+    i = _cpu(ids).to(torch.int64).contiguous()
+    b = _cpu(blocks).to(torch.float32).contiguous()
+    n, d = b.shape
+    sums = torch.empty(k, d, dtype=torch.float32)
+    counts = torch.empty(k, dtype=torch.int64)
+    if lib().or_centroid_sums(i.data_ptr(), n, b.data_ptr(), d, k, sums.data_ptr(), counts.data_ptr()) != 0:
+        raise IndexError("ids outside [0, k)")
+    return sums, counts

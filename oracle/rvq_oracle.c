@@ -318,3 +318,20 @@ void or_assign(const float* blocks, int64_t n, int d, const float* codebook, int
     min_dist[i] = best_d;
   }
 }
+
+/* _fit_kmeans centroid reductions, src/block_vq.py:216-218 (see rvq_oracle.h). */
+int or_centroid_sums(const int64_t* ids, int64_t n, const float* blocks, int d, int64_t k_cb,
+                     float* sums, int64_t* counts) {
+  for (int64_t i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= k_cb) return -1;
+  for (int64_t k = 0; k < k_cb; ++k) {
+    counts[k] = 0;
+    for (int j = 0; j < d; ++j) sums[k * d + j] = 0.0f;
+  }
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t k = ids[i];
+    counts[k] += 1;
+    for (int j = 0; j < d; ++j) sums[k * d + j] = sums[k * d + j] + blocks[i * d + j];
+  }
+  return 0;
+}

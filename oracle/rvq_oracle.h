@@ -121,6 +121,15 @@ void or_id_route_weight(const void* ids, int id_dtype, int64_t n_rows, int64_t k
 void or_assign(const float* blocks, int64_t n, int d, const float* codebook, int64_t k_cb,
                int64_t* ids, float* min_dist);
 
+/* The centroid update's reductions in _fit_kmeans (src/block_vq.py:216-218):
+ *   counts = bincount(ids, minlength=k_cb);
+ *   sums = zeros(k_cb, d).index_add_(0, ids, blocks)
+ * with torch's CPU order: for i = 0..n-1 ascending, sums[ids[i]][j] += blocks[i][j]
+ * in fp32 from +0.  ids must lie in [0, k_cb) (returns -1 otherwise, like
+ * index_add_ raising). */
+int or_centroid_sums(const int64_t* ids, int64_t n, const float* blocks, int d, int64_t k_cb,
+                     float* sums, int64_t* counts);
+
 #ifdef __cplusplus
 }
 #endif

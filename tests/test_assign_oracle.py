@@ -90,3 +90,27 @@ def test_assign_wrapper_validates_like_the_reference():
         _assign_to_codebook(torch.empty(0, 8), torch.zeros(4, 8))
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         _assign_to_codebook(torch.zeros(4, 8), torch.zeros(4, 8))
+
+
+@pytest.mark.parametrize("d", [1, 8, 32])
+def test_centroid_sums_match_reference_ops(d):
+    """or_centroid_sums against the reference's own update ops run by torch on
+    the CPU (src/block_vq.py:216-218): bincount and index_add_, bit for bit,
+    with an empty cluster and a heavy one; and against float64 sums."""
+    g = torch.Generator().manual_seed(d)
+    n, k = 6000, 97
+    b = torch.randn(n, d, generator=g)
+    ids = torch.randint(0, k, (n,), generator=g)
+    ids[ids == 5] = 6          # cluster 5 empty
+    ids[:1500] = 11            # cluster 11 heavy
+    sums, counts = c_oracle.centroid_sums(ids, b, k)
+    assert torch.equal(counts, torch.bincount(ids, minlength=k))
+    assert torch.equal(sums, torch.zeros(k, d).index_add_(0, ids, b))
+    assert counts[5] == 0 and torch.all(sums[5] == 0)
+    exact = torch.zeros(k, d, dtype=torch.float64).index_add_(0, ids, b.double())
+    assert float((sums.double() - exact).abs().max()) < 1e-3
+
+
+def test_centroid_sums_rejects_bad_ids():
+    with pytest.raises(IndexError):
+        c_oracle.centroid_sums(torch.tensor([0, 3]), torch.zeros(2, 4), 3)

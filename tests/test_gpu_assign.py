@@ -84,3 +84,49 @@ def test_assign_errors(gpu_device):
         _assign_to_codebook(torch.empty(0, 8, device=gpu_device), torch.zeros(4, 8, device=gpu_device))
     with pytest.raises(_lib.WalError):
         _assign_to_codebook(torch.zeros(4, 3, device=gpu_device), torch.zeros(4, 3, device=gpu_device))
+
+
+@pytest.mark.parametrize("d", [1, 8, 32])
+@pytest.mark.parametrize("k", [1, 7, 256, 1000])
+@pytest.mark.parametrize("n", [0, 1, 1000, 70000])
+def test_centroid_sums_bitexact(d, k, n, gpu_device):
+    """wal_rvq_centroid_sums against or_centroid_sums (ascending block order),
+    with a heavy cluster and empty ones."""
+    from wal2026_amd.block_vq import _centroid_sums
+
+    print(f"centroid sums n={n} d={d} k={k}", flush=True)
+    g = torch.Generator().manual_seed(n + d + k)
+    b = torch.randn(n, d, generator=g)
+    ids = torch.randint(0, k, (n,), generator=g)
+    if n >= 1000:
+        ids[: n // 3] = k - 1
+    sums, counts = _centroid_sums(ids.to(gpu_device), b.to(gpu_device), k)
+    ref_sums, ref_counts = c_oracle.centroid_sums(ids, b, k)
+    assert torch.equal(counts.cpu(), ref_counts)
+    assert torch.equal(sums.cpu().view(torch.int32), ref_sums.view(torch.int32))
+
+
+def test_centroid_sums_rejects_out_of_range_ids(gpu_device):
+    from wal2026_amd.block_vq import _centroid_sums
+
+    with pytest.raises(IndexError):
+        _centroid_sums(torch.tensor([0, 5], device=gpu_device), torch.zeros(2, 8, device=gpu_device), 5)
+
+
+def test_fit_kmeans_iteration_matches_oracle(gpu_device):
+    """One GPU Lloyd iteration (_fit_kmeans) equals the oracle's assignment,
+    sums and the fp32 mean applied to the same initial codebook."""
+    from wal2026_amd.block_vq import _fit_kmeans
+
+    g = torch.Generator().manual_seed(21)
+    blocks = torch.randn(20000, 8, generator=g) * 0.02
+    dev_blocks = blocks.to(gpu_device)
+    init = _fit_kmeans(dev_blocks, 64, iters=0).cpu()
+    got = _fit_kmeans(dev_blocks, 64, iters=1).cpu()
+    ids, _ = c_oracle.assign(blocks, init)
+    sums, counts = c_oracle.centroid_sums(ids, blocks, 64)
+    assert torch.all(counts > 0)
+    want = sums / counts.to(torch.float32)[:, None]
+    assert torch.equal(got, want)
+    cb = _fit_kmeans(dev_blocks, 64, iters=4)
+    assert cb.shape == (64, 8) and torch.isfinite(cb).all()

@@ -215,9 +215,70 @@ def _assign_to_codebook(blocks: Tensor, codebook: Tensor, batch_size: int = 16_3
     return ids, dist
 
 
+def _centroid_sums(ids: Tensor, blocks: Tensor, k: int) -> tuple[Tensor, Tensor]:
+    """``(sums [k, d] fp32, counts [k] int64)`` of the k-means update on the GPU
+    (``wal_rvq_centroid_sums``): ``counts = bincount(ids, minlength=k)`` and
+    ``sums = zeros(k, d).index_add_(0, ids, blocks)`` with every sum taken in
+    ascending block order, as torch's CPU ``index_add_`` adds (reference
+    src/block_vq.py:216-218); deterministic, unlike atomics."""
+    from . import _lib
+
+    dev = _lib.require_rocm(ids, blocks)
+    ids = ids.to(torch.int64).contiguous()
+    b = blocks.to(torch.float32).contiguous()
+    n, d = b.shape
+    if ids.shape != (n,):
+        raise ValueError(f"ids must have shape ({n},), got {tuple(ids.shape)}")
+    if n:
+        lo, hi = torch.stack([ids.min(), ids.max()]).tolist()
+        if lo < 0 or hi >= k:
+            raise IndexError(f"ids hold index range [{lo}, {hi}] outside [0, {k})")
+    sums = torch.empty(k, d, dtype=torch.float32, device=dev)
+    counts = torch.empty(k, dtype=torch.int64, device=dev)
+    _lib.check(_lib.lib().wal_rvq_centroid_sums(ids.data_ptr(), n, b.data_ptr(), d, k, sums.data_ptr(),
+                                                counts.data_ptr(), _lib.stream_ptr(dev)))
+    return sums, counts
+
+
+def _fit_kmeans(blocks: Tensor, codebook_size: int, iters: int, batch_size: int = 16_384) -> Tensor:
+    """Lloyd's k-means on the GPU, the reference's ``_fit_kmeans``
+    (src/block_vq.py:199-227): initial codewords are the blocks at the first
+    ``codebook_size`` positions of a permutation drawn from a generator on the
+    blocks' device seeded with 0; every iteration assigns each block to its
+    nearest codeword (``_assign_to_codebook``), replaces each non-empty
+    cluster's codeword by its mean (``_centroid_sums``, then the fp32 division)
+    and reseeds empty clusters from blocks drawn with the same generator."""
+    del batch_size
+    if blocks.ndim != 2:
+        raise ValueError("expected 2D blocks")
+    if blocks.shape[0] < codebook_size:
+        raise ValueError("sample set must be at least as large as codebook_size")
+    blocks = blocks.to(torch.float32)
+    gen = torch.Generator(device=blocks.device)
+    gen.manual_seed(0)
+    first = torch.randperm(blocks.shape[0], generator=gen, device=blocks.device)[:codebook_size]
+    codebook = blocks[first].clone()
+    for _ in range(iters):
+        ids, _ = _assign_to_codebook(blocks, codebook)
+        sums, counts = _centroid_sums(ids, blocks, codebook_size)
+        filled = counts > 0
+        new = codebook.clone()
+        new[filled] = sums[filled] / counts[filled].to(torch.float32)[:, None]
+        empty = torch.nonzero(~filled).flatten()
+        if empty.numel():
+            pick = torch.randint(0, blocks.shape[0], (empty.numel(),), generator=gen, device=blocks.device)
+            new[empty] = blocks[pick]
+        codebook = new
+    return codebook
+
+
 def _kmeans(sample: Tensor, k: int, iters: int, batch_size: int) -> Tensor:
     """Lloyd iterations from a seeded random subset; empty clusters are
-    reseeded from random samples."""
+    reseeded from random samples.  On a ROCm device this is ``_fit_kmeans``
+    (HIP assignment and centroid sums); a CPU sample (the encoder also runs
+    offline on the host) takes torch's expression of the same steps."""
+    if sample.is_cuda:
+        return _fit_kmeans(sample, k, iters, batch_size)
     if sample.shape[0] < k:
         raise ValueError("sample set must be at least as large as codebook_size")
     sample = sample.to(torch.float32)
@@ -225,9 +286,7 @@ def _kmeans(sample: Tensor, k: int, iters: int, batch_size: int) -> Tensor:
     gen.manual_seed(0)
     cb = sample[torch.randperm(sample.shape[0], generator=gen, device=sample.device)[:k]].clone()
     for _ in range(iters):
-        # on a ROCm device the assignment is the HIP kernel; a CPU sample (the
-        # encoder runs offline) takes the torch expression of the same formula
-        ids, _ = _assign_to_codebook(sample, cb) if sample.is_cuda else _nearest(sample, cb, batch_size)
+        ids, _ = _nearest(sample, cb, batch_size)
         counts = torch.bincount(ids, minlength=k)
         sums = torch.zeros_like(cb).index_add_(0, ids, sample)
         filled = counts > 0

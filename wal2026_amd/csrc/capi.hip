@@ -507,4 +507,16 @@ int wal_rvq_assign(const float* blocks, int64_t n, int d, const float* codebook,
   return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_assign launch");
 }
 
+int wal_rvq_centroid_sums(const int64_t* ids, int64_t n, const float* blocks, int d, int64_t k_cb, float* sums,
+                          int64_t* counts, void* stream) {
+  g_err[0] = 0;
+  if (n < 0) return fail(WAL_EINVAL, "n must be >= 0 (got %lld)", (long long)n);
+  if ((n > 0 && (!ids || !blocks)) || !sums || !counts) return fail(WAL_EINVAL, "NULL buffer");
+  if (!(d == 1 || d == 2 || d == 4 || d == 8 || d == 16 || d == 32))
+    return fail(WAL_EUNSUPPORTED, "block size %d not supported (1, 2, 4, 8, 16 or 32)", d);
+  if (k_cb < 1 || k_cb > 0x7fffffff) return fail(WAL_EINVAL, "codebook size must be in [1, 2^31) (got %lld)", (long long)k_cb);
+  hipError_t e = launch_centroid_sums(ids, n, blocks, d, (int)k_cb, sums, counts, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_centroid_sums launch");
+}
+
 }  // extern "C"

@@ -134,7 +134,75 @@ hipError_t assign_go(const float* blocks, int64_t n, const float* codebook, int 
   return hipGetLastError();
 }
 
+// ---- centroid sums of the k-means update --------------------------------
+// One workgroup per codeword k scans the ids in chunks of 256 blocks, keeps
+// the chunk's matching block indices in LDS in block order (wave ballots and
+// an exclusive count over the waves), and threads j < D add column j of those
+// blocks one after another: sums[k][j] is the fp32 sum from +0 in ascending
+// block order, which is the order torch's CPU index_add_ uses
+// (src/block_vq.py:216-218), and counts[k] the number of matches (bincount).
+constexpr int kSumThreads = 256;
+
+template <int D>
+__global__ __launch_bounds__(kSumThreads) void rvq_centroid_sums_kernel(const int64_t* __restrict__ ids, int64_t n,
+                                                                        const float* __restrict__ blocks,
+                                                                        float* __restrict__ sums,
+                                                                        int64_t* __restrict__ counts) {
+  __shared__ int64_t list[kSumThreads];
+  __shared__ int wcount[kSumThreads / 64];
+  const int64_t k = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float acc = 0.0f;  // column tid, for tid < D
+  int64_t cnt = 0;
+  int64_t next_id = tid < n ? ids[tid] : -1;  // the id of this thread's block in the next chunk
+  for (int64_t c0 = 0; c0 < n; c0 += kSumThreads) {
+    const int64_t i = c0 + tid;
+    const bool match = next_id == k;  // (-1 past the end never matches)
+    const int64_t i2 = i + kSumThreads;
+    next_id = i2 < n ? ids[i2] : -1;
+    const unsigned long long mask = __ballot(match);
+    if (lane == 0) wcount[wave] = __popcll(mask);
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kSumThreads / 64; ++w) {
+      const int cw = wcount[w];
+      before += w < wave ? cw : 0;
+      total += cw;
+    }
+    if (match) list[before + __popcll(mask & ((1ull << lane) - 1ull))] = i;
+    __syncthreads();
+    if (tid < D)
+      for (int m = 0; m < total; ++m) acc = acc + blocks[list[m] * D + tid];
+    cnt += total;
+    __syncthreads();  // list and wcount are rewritten by the next chunk
+  }
+  if (tid < D) sums[k * D + tid] = acc;
+  if (tid == 0) counts[k] = cnt;
+}
+
+template <int D>
+hipError_t centroid_sums_go(const int64_t* ids, int64_t n, const float* blocks, int K, float* sums, int64_t* counts,
+                            hipStream_t st) {
+  hipLaunchKernelGGL((rvq_centroid_sums_kernel<D>), dim3((unsigned)K), dim3(kSumThreads), 0, st, ids, n, blocks, sums,
+                     counts);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_centroid_sums(const int64_t* ids, int64_t n, const float* blocks, int d, int K, float* sums,
+                                int64_t* counts, hipStream_t st) {
+  switch (d) {
+    case 1: return centroid_sums_go<1>(ids, n, blocks, K, sums, counts, st);
+    case 2: return centroid_sums_go<2>(ids, n, blocks, K, sums, counts, st);
+    case 4: return centroid_sums_go<4>(ids, n, blocks, K, sums, counts, st);
+    case 8: return centroid_sums_go<8>(ids, n, blocks, K, sums, counts, st);
+    case 16: return centroid_sums_go<16>(ids, n, blocks, K, sums, counts, st);
+    case 32: return centroid_sums_go<32>(ids, n, blocks, K, sums, counts, st);
+    default: return hipErrorInvalidValue;  // excluded by the entry point's checks
+  }
+}
 
 hipError_t launch_assign(const float* blocks, int64_t n, int d, const float* codebook, int K, int64_t* ids,
                          float* min_dist, hipStream_t st) {

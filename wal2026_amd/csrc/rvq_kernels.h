@@ -99,6 +99,10 @@ extern template hipError_t prefill_entry<WAL_F16, uint16_t>(const LayerArgs&, co
 hipError_t launch_assign(const float* blocks, int64_t n, int d, const float* codebook, int K, int64_t* ids,
                          float* min_dist, hipStream_t st);
 
+// k-means centroid sums and counts (block order), rvq_assign.hip.
+hipError_t launch_centroid_sums(const int64_t* ids, int64_t n, const float* blocks, int d, int K, float* sums,
+                                int64_t* counts, hipStream_t st);
+
 inline hipError_t launch_decode(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
                                 int lds_mode, const void* x, int M, int n_cu, hipStream_t st) {
   if (L.n_tiles == 0) return hipSuccess;
