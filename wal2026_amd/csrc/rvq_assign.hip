@@ -117,10 +117,9 @@ __global__ __launch_bounds__(kAssignThreads) void rvq_assign_kernel(const float*
   }
 }
 
-template <int D>
-hipError_t assign_go(const float* blocks, int64_t n, const float* codebook, int K, int64_t* ids, float* min_dist,
-                     hipStream_t st) {
-  constexpr int R = assign_rows<D>();
+template <int D, int R>
+hipError_t assign_launch(const float* blocks, int64_t n, const float* codebook, int K, int64_t* ids, float* min_dist,
+                         hipStream_t st) {
   // entries per LDS chunk: a multiple of the workgroup size, at most K
   int kc = kAssignLdsBytes / ((D + 1) * (int)sizeof(float));
   kc = kc >= kAssignThreads ? kc - kc % kAssignThreads : kc;
@@ -132,6 +131,20 @@ hipError_t assign_go(const float* blocks, int64_t n, const float* codebook, int 
   hipLaunchKernelGGL((rvq_assign_kernel<D, R>), dim3((unsigned)grid), dim3(kAssignThreads), lds, st, blocks, n,
                      codebook, K, kc, ids, min_dist);
   return hipGetLastError();
+}
+
+// R blocks per thread amortise each LDS codeword read over R distances; a
+// launch too small to give every CU a few workgroups that way takes one block
+// per thread instead (kAssignMinGrid: 4 workgroups for each of 256 CUs).
+constexpr int64_t kAssignMinGrid = 1024;
+
+template <int D>
+hipError_t assign_go(const float* blocks, int64_t n, const float* codebook, int K, int64_t* ids, float* min_dist,
+                     hipStream_t st) {
+  constexpr int R = assign_rows<D>();
+  if (R > 1 && (n + (int64_t)kAssignThreads * R - 1) / ((int64_t)kAssignThreads * R) < kAssignMinGrid)
+    return assign_launch<D, 1>(blocks, n, codebook, K, ids, min_dist, st);
+  return assign_launch<D, R>(blocks, n, codebook, K, ids, min_dist, st);
 }
 
 // ---- centroid sums of the k-means update --------------------------------
