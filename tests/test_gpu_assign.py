@@ -130,3 +130,24 @@ def test_fit_kmeans_iteration_matches_oracle(gpu_device):
     assert torch.equal(got, want)
     cb = _fit_kmeans(dev_blocks, 64, iters=4)
     assert cb.shape == (64, 8) and torch.isfinite(cb).all()
+
+
+def test_encoder_on_gpu(gpu_device):
+    """The offline encoder on a ROCm device (HIP assignment and centroid sums
+    inside): shapes and storage dtypes as on the CPU, a sensible fit, and two
+    runs give identical encodings (no atomics in the reductions)."""
+    from wal2026_amd import block_vq as w
+
+    g = torch.Generator().manual_seed(0)
+    weight = torch.randn(64, 40, generator=g).to(gpu_device)
+    kw = dict(group_rows=32, block_size=8, codebook_size=32, num_stages=2, sample_limit=4096, kmeans_iters=4)
+    a = w.encode_grouped_block_residual_vq(weight, **kw)
+    b = w.encode_grouped_block_residual_vq(weight, **kw)
+    assert len(a.groups) == 2 and a.groups[0].stage_ids[0].shape == (32, 5)
+    assert a.groups[0].stage_ids[0].dtype == torch.uint8
+    assert 0.0 < a.sample_rel_mse < 0.5
+    for ga, gb in zip(a.groups, b.groups):
+        for sa, sb in zip(ga.stage_ids, gb.stage_ids):
+            assert torch.equal(sa, sb)
+        for ca, cb in zip(ga.codebooks, gb.codebooks):
+            assert torch.equal(ca, cb)

@@ -240,6 +240,18 @@ def _centroid_sums(ids: Tensor, blocks: Tensor, k: int) -> tuple[Tensor, Tensor]
     return sums, counts
 
 
+_HIP_ASSIGN_DIMS = (1, 2, 4, 8, 16, 32)
+
+
+def _assign(blocks: Tensor, codebook: Tensor, batch_size: int) -> tuple[Tensor, Tensor]:
+    """The encoder's assignment: the HIP kernel on a ROCm device for the block
+    widths it covers, torch's expression of the same formula otherwise (CPU
+    samples, unusual product-split widths)."""
+    if blocks.is_cuda and blocks.shape[1] in _HIP_ASSIGN_DIMS:
+        return _assign_to_codebook(blocks, codebook)
+    return _nearest(blocks, codebook, batch_size)
+
+
 def _fit_kmeans(blocks: Tensor, codebook_size: int, iters: int, batch_size: int = 16_384) -> Tensor:
     """Lloyd's k-means on the GPU, the reference's ``_fit_kmeans``
     (src/block_vq.py:199-227): initial codewords are the blocks at the first
@@ -277,7 +289,7 @@ def _kmeans(sample: Tensor, k: int, iters: int, batch_size: int) -> Tensor:
     reseeded from random samples.  On a ROCm device this is ``_fit_kmeans``
     (HIP assignment and centroid sums); a CPU sample (the encoder also runs
     offline on the host) takes torch's expression of the same steps."""
-    if sample.is_cuda:
+    if sample.is_cuda and sample.shape[1] in _HIP_ASSIGN_DIMS:
         return _fit_kmeans(sample, k, iters, batch_size)
     if sample.shape[0] < k:
         raise ValueError("sample set must be at least as large as codebook_size")
@@ -374,9 +386,9 @@ def encode_block_residual_vq(
         lo, hi = split * sub, (split + 1) * sub
         for _ in range(count):
             cb = _kmeans(sample[:, lo:hi], codebook_size, kmeans_iters, batch_size)
-            ids, _ = _nearest(residual[:, lo:hi], cb, batch_size)
+            ids, _ = _assign(residual[:, lo:hi], cb, batch_size)
             residual[:, lo:hi] -= cb[ids]
-            sids, _ = _nearest(sample[:, lo:hi], cb, batch_size)
+            sids, _ = _assign(sample[:, lo:hi], cb, batch_size)
             sample[:, lo:hi] -= cb[sids]
             full = torch.zeros(codebook_size, block_size, dtype=torch.float32, device=residual.device)
             full[:, lo:hi] = cb
