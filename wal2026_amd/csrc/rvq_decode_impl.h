@@ -261,11 +261,24 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   // x fragments (zero past the row) are read once: XM_GREG here, from global
   // memory, XM_REG after the barrier, from the x rows staged in LDS.
   u32x4_t xreg[XREG ? 16 : 1];
+  // XM_GREG with room in the table slots (uniform): each load reads one
+  // contiguous 1 KB run of an x row (lane = block of the wave's chunk), and
+  // the fragments are transposed through the table slots' LDS before the
+  // tables are staged.  A lane's own fragments are 16-byte pieces of one row,
+  // so loading them directly touches 64 cache lines per instruction.
+  const bool xt = XMODE == XM_GREG && M > 4 && (size_t)nslots * tbl_bytes >= (size_t)NW * 16 * 1024;
   if constexpr (XMODE == XM_GREG) {
-    const int base = wave * 64 + 16 * q;
+    if (xt) {
+      const int blk = wave * 64 + lane;
 #pragma unroll
-    for (int tt = 0; tt < 16; ++tt)
-      xreg[tt] = base < B ? ldg128(x + (size_t)xm * in + (size_t)(base + tt) * 8) : u32x4_t{0, 0, 0, 0};
+      for (int u = 0; u < 16; ++u)
+        if (u < M) xreg[u] = blk < B ? ldg128(x + (size_t)u * in + (size_t)blk * 8) : u32x4_t{0, 0, 0, 0};
+    } else {
+      const int base = wave * 64 + 16 * q;
+#pragma unroll
+      for (int tt = 0; tt < 16; ++tt)
+        xreg[tt] = base < B ? ldg128(x + (size_t)xm * in + (size_t)(base + tt) * 8) : u32x4_t{0, 0, 0, 0};
+    }
   }
   u32x4_t b0[kImageBatch], b1[kImageBatch];
   if (have_image) {
@@ -313,6 +326,22 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   for (int j = 0; j < PF; ++j) issue(j);
 
   // ---- prologue, part 2: stage the tables and x while the ring loads fly ---
+  if constexpr (XMODE == XM_GREG) {
+    if (xt) {
+      // this wave's rows of its chunk, 1 KB per row, piece p of row u at
+      // p ^ u: conflict-free writes, and conflict-free reads for the 16
+      // lanes (16 rows) of each read pass
+      uint8_t* xw = lds_cb + (size_t)wave * 16 * 1024;
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (u < M) *reinterpret_cast<u32x4_t*>(xw + u * 1024 + ((lane ^ u) & 63) * 16) = xreg[u];
+      // (a wave reads back only what it wrote)
+#pragma unroll
+      for (int tt = 0; tt < 16; ++tt)
+        xreg[tt] = *reinterpret_cast<const u32x4_t*>(xw + xm * 1024 + (((16 * q + tt) ^ xm) & 63) * 16);
+      __syncthreads();  // every wave holds its fragments before the tables overwrite the slots
+    }
+  }
   if (tid < 16) reinterpret_cast<u32x4_t*>(zrow)[tid] = u32x4_t{0, 0, 0, 0};
   RowScale r0 = make_row_scale<XDT>(0.0f), r1 = r0;
   if constexpr (SCALED) {
