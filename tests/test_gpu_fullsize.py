@@ -87,3 +87,26 @@ def test_full_prefill_parity_sampled_rows(tile, gpu_device, monkeypatch):
     w_ref = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
     ref = c_oracle.linear_f64(x[rows], w_ref)
     assert rel_err(y[rows], ref) <= TOL
+
+
+@pytest.mark.parametrize("m", [5, 9, 16])
+def test_full_decode_down_proj_transposed_x(m, gpu_device):
+    """c3 down_proj (4096 x 14336) at 4 < M <= 16: x (up to 458 KB) fits
+    neither LDS nor registers, so each item's x fragments are loaded as row
+    runs and transposed through a per-wave LDS scratch, one or two 8-row
+    halves (M = 5: one half; 9: a partial second half; 16: both full)."""
+    print(f"[fullsize] decode c3_down m={m}", flush=True)
+    cfg, mod, gen = _layer("c3", 4096, 14336, gpu_device)
+    x = synth.make_activation(m, 14336, cfg.x_dtype, gen)
+    y = mod._hip_linear(x.to(gpu_device), fast=False, out_dtype=torch.float32)
+    w_ref = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
+    assert rel_err(y, c_oracle.linear_f64(x, w_ref)) <= TOL
+    # one-hot rows read the kernel's weights out exactly: columns spread over
+    # the row, including the first and last block of a chunk
+    cols = [0, 7, 8, 511, 512, 4095, 7000, 14335][: m]
+    eye = torch.zeros(m, 14336, dtype=cfg.x_dtype)
+    for i, c in enumerate(cols):
+        eye[i, c] = 1.0
+    got = mod._hip_linear(eye.to(gpu_device), fast=False, out_dtype=torch.float32).cpu()
+    for i, c in enumerate(cols):
+        assert torch.equal(got[i], w_ref[:, c].float()), (m, c)

@@ -67,11 +67,14 @@ WAL_DEVICE uint32_t extract_id(const u32x4_t (&v)[sizeof(IdT)], int t) {
 // the output rows of every tile (max_tiles tiles per workgroup), a 256-byte
 // zero row and (xlds) the activation rows.
 constexpr int kDecodeTileMetaBytes = 16;  // {out_row0, rows, -, -} per tile
+// xscr: the per-wave x transpose scratch of XM_GTR (8 rows x 1 KB a wave).
+constexpr int kDecodeXScratchBytes = 8 * 1024;
 template <int LMODE>
-WAL_HOST_DEVICE size_t decode_lds_bytes(int S, int K, bool xlds, int M, int in, int nw, int max_tiles, int nslots) {
+WAL_HOST_DEVICE size_t decode_lds_bytes(int S, int K, bool xlds, int M, int in, int nw, int max_tiles, int nslots,
+                                        bool xscr = false) {
   return (size_t)nslots * S * K * lds_entry_bytes<LMODE>() +
          (size_t)max_tiles * (nw * M * 16 * sizeof(float) + kDecodeTileMetaBytes) + 256 +
-         (xlds ? (size_t)M * in * sizeof(uint16_t) : 0);
+         (xlds ? (size_t)M * in * sizeof(uint16_t) : 0) + (xscr ? (size_t)nw * kDecodeXScratchBytes : 0);
 }
 
 // Tile metadata through the scalar cache (uniform t): no vector-memory
@@ -162,8 +165,12 @@ enum XMode : int {
   XM_LDS = 1,     // x staged in LDS, fragments read per item
   XM_REG = 2,     // x staged in LDS; each wave owns one chunk (CPT == 1), so its
                   // 16 fragments are read once and kept in registers
-  XM_GREG = 3     // as XM_REG, but the 16 fragments come straight from global
+  XM_GREG = 3,    // as XM_REG, but the 16 fragments come straight from global
                   // memory (large M: x beside two tables would not fit LDS)
+  XM_GTR = 4      // M > 4, x too large for LDS: per item, each load reads one
+                  // contiguous 1 KB run of an x row and the fragments are
+                  // transposed through a per-wave LDS scratch (XM_GLOBAL's
+                  // direct fragment loads touch 64 cache lines each)
 };
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int XMODE, bool SCALED>
@@ -193,6 +200,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   int* tmeta = reinterpret_cast<int*>(part + (size_t)max_tiles * NW * M16);      // [max_tiles][4]
   uint8_t* zrow = reinterpret_cast<uint8_t*>(tmeta + (size_t)max_tiles * 4);   // 256 zero bytes
   uint16_t* xs = reinterpret_cast<uint16_t*>(zrow + 256);                    // [M][in] when XLDS
+  uint8_t* xscr = zrow + 256;  // XM_GTR: [NW][8 rows][1 KB] transpose scratch
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -440,6 +448,15 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
         const uint8_t* xp = XLDS && seg_ok ? reinterpret_cast<const uint8_t*>(xs + (size_t)xm * in + (size_t)base * 8)
                                            : zrow;
         const uint8_t* tbl = lds_cb + (size_t)slot * tbl_bytes;
+        // XM_GTR: the rows' runs of this chunk, issued before the gathers so
+        // their latency runs under them
+        u32x4_t xv[XMODE == XM_GTR ? 16 : 1];
+        if constexpr (XMODE == XM_GTR) {
+          const int blk = c * 64 + lane;
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            if (u < M) xv[u] = blk < B ? ldg128(x + (size_t)u * in + (size_t)blk * 8) : u32x4_t{0, 0, 0, 0};
+        }
         // All 16 fragments of the item are gathered before the first MFMA
         // consumes one, so the LDS latency is paid once per item instead of
         // once per block.
@@ -454,11 +471,36 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
         }
         // keep the scheduler from sinking the gathers back next to their MFMAs
         __builtin_amdgcn_sched_barrier(0);
+        // XM_GTR: rows 0-7, then 8-15, through this wave's 8 KB scratch (piece
+        // p of row r at p ^ r: conflict-free writes, and conflict-free reads
+        // for the 16 lanes of a read pass); each lane reads in the half that
+        // holds its row.  LDS operations of one wave complete in order, so
+        // the second half's writes do not overtake the first half's reads.
+        u32x4_t xt[XMODE == XM_GTR ? 16 : 1];
+        if constexpr (XMODE == XM_GTR) {
+          uint8_t* sw = xscr + (size_t)wave * kDecodeXScratchBytes;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            if (8 * h < M) {
+#pragma unroll
+              for (int u = 0; u < 8; ++u)
+                if (8 * h + u < M)
+                  *reinterpret_cast<u32x4_t*>(sw + u * 1024 + ((lane ^ (8 * h + u)) & 63) * 16) = xv[8 * h + u];
+              if ((xm >> 3) == h) {
+#pragma unroll
+                for (int tt = 0; tt < 16; ++tt)
+                  xt[tt] = *reinterpret_cast<const u32x4_t*>(sw + (xm - 8 * h) * 1024 + (((16 * q + tt) ^ xm) & 63) * 16);
+              }
+            }
+          }
+        }
 #pragma unroll
         for (int tt = 0; tt < 16; ++tt) {
           u32x4_t xf;
           if constexpr (XREG) {
             xf = xreg[tt];
+          } else if constexpr (XMODE == XM_GTR) {
+            xf = xt[tt];
           } else if constexpr (XMODE == XM_LDS) {
             xf = *reinterpret_cast<const u32x4_t*>(xp + tt * 16);
           } else {
@@ -506,8 +548,8 @@ static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const Epilog
   // Each workgroup takes an equal share of the tiles and keeps the partial
   // sums of its whole share in LDS; when a share does not fit, the grid grows
   // until it does.
-  auto plan_for = [&](int nslots, bool xlds, int* grid, int* share) -> bool {
-    const size_t fixed = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, 0, nslots);
+  auto plan_for = [&](int nslots, bool xlds, bool xscr, int* grid, int* share) -> bool {
+    const size_t fixed = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, 0, nslots, xscr);
     const size_t per_tile = (size_t)nw * M * 16 * sizeof(float) + kDecodeTileMetaBytes;
     if (fixed + per_tile > (size_t)kLdsMax) return false;
     const int fit = (int)(((size_t)kLdsMax - fixed) / per_tile);
@@ -530,13 +572,14 @@ static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const Epilog
   const bool one_chunk = nchunk <= nw;
   struct Cand { int xmode, nslots; };
   const Cand cands[] = {{one_chunk ? XM_REG : XM_LDS, 2}, {XM_GREG, 2}, {one_chunk ? XM_REG : XM_LDS, 1},
-                        {XM_GREG, 1}, {XM_GLOBAL, 2}, {XM_GLOBAL, 1}};
+                        {XM_GREG, 1}, {XM_GTR, 2}, {XM_GTR, 1}, {XM_GLOBAL, 2}, {XM_GLOBAL, 1}};
   int grid = 0, share = 1, nslots = 0, xmode = XM_GLOBAL, best_rounds = 1 << 30;
   for (const Cand& c : cands) {
     if (c.nslots == 2 && !segments) continue;
     if (c.xmode == XM_GREG && !one_chunk) continue;
+    if (c.xmode == XM_GTR && M <= 4) continue;  // up to 4 rows, direct loads touch at most 16 lines
     int g = 0, sh = 1;
-    if (!plan_for(c.nslots, c.xmode == XM_REG || c.xmode == XM_LDS, &g, &sh)) continue;
+    if (!plan_for(c.nslots, c.xmode == XM_REG || c.xmode == XM_LDS, c.xmode == XM_GTR, &g, &sh)) continue;
     const int rounds = (g + n_cu - 1) / n_cu;
     if (rounds < best_rounds) {
       best_rounds = rounds;
@@ -546,13 +589,14 @@ static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const Epilog
   }
   if (nslots == 0) return hipErrorInvalidValue;  // excluded by the host's eligibility check
   const bool xlds = xmode == XM_REG || xmode == XM_LDS;
-  const size_t lds = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, share, nslots);
+  const size_t lds = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, share, nslots, xmode == XM_GTR);
   if (grid < 1) return hipSuccess;
   auto kern = xmode == XM_REG    ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_REG, SCALED>
               : xmode == XM_LDS  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_LDS, SCALED>
               : xmode == XM_GREG ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GREG, SCALED>
+              : xmode == XM_GTR  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GTR, SCALED>
                                  : rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GLOBAL, SCALED>;
-  static bool attr_set[4] = {false, false, false, false};
+  static bool attr_set[5] = {false, false, false, false, false};
   if (!attr_set[xmode]) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                        kLdsMax);
