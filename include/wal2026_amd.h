@@ -18,6 +18,13 @@
  *  - Nothing here allocates device memory or synchronises the stream.
  *  - Tensors are dense and row-major.  Element types are given by wal_dtype
  *    tags.
+ *  - Index values are NOT range-checked on the device: every id must lie in
+ *    [0, codebook_size) (the reference's gather would raise on a bad id).
+ *    Checking them needs a pass over the index planes, so the library leaves
+ *    it to the caller (the Python layer checks once per module).  An id at or
+ *    past codebook_size is clamped to codebook_size - 1 by every kernel, so a
+ *    bad id gives a wrong but deterministic result, the same at every m;
+ *    it never reads outside the codebook.
  */
 #ifndef WAL2026_AMD_H
 #define WAL2026_AMD_H
@@ -30,7 +37,7 @@ extern "C" {
 #endif
 
 #define WAL_RVQ_MAX_STAGES 8
-#define WAL_ABI_VERSION 2
+#define WAL_ABI_VERSION 3
 
 typedef enum wal_dtype {
   WAL_U8 = 0,   /* index planes, codebook_size <= 256 (src/block_vq.py:160-165) */
@@ -231,6 +238,48 @@ int wal_rvq_assign(const float* blocks, int64_t n, int d, const float* codebook,
  * int64 (zeros when n = 0). */
 int wal_rvq_centroid_sums(const int64_t* ids, int64_t n, const float* blocks, int d, int64_t k_cb,
                           float* sums, int64_t* counts, void* stream);
+
+/* ---- launch planning (diagnostics) ---------------------------------------- */
+
+/* Kernel families of wal_rvq_linear. */
+#define WAL_KERNEL_NONE 0     /* m == 0: nothing to launch */
+#define WAL_KERNEL_DECODE 1   /* block-size-8 MFMA decode kernel, m <= 16 */
+#define WAL_KERNEL_PREFILL 2  /* block-size-8 MFMA prefill kernel, m > 16 */
+#define WAL_KERNEL_GENERIC 3  /* any other layout or semantics */
+
+/* Where the decode kernel's activation fragments come from. */
+#define WAL_XMODE_GLOBAL 0  /* global memory (L2), per item */
+#define WAL_XMODE_LDS 1     /* x rows staged in LDS, per item */
+#define WAL_XMODE_REG 2     /* staged in LDS, held in registers (one chunk per wave) */
+#define WAL_XMODE_GREG 3    /* global memory into registers once (one chunk per wave) */
+#define WAL_XMODE_GTR 4     /* row runs from global memory, transposed through LDS per item */
+
+/* Prefill tile shapes (x rows x weight rows per workgroup). */
+#define WAL_TILE_SHORT 0  /* 128 x 256 */
+#define WAL_TILE_TALL 1   /* 256 x 256 */
+#define WAL_TILE_WIDE 2   /* 256 x 128 */
+
+typedef struct wal_rvq_launch_info {
+  int32_t kernel;       /* WAL_KERNEL_* */
+  int32_t x_mode;       /* decode: WAL_XMODE_*; else -1 */
+  int32_t table_slots;  /* decode: codebook tables a workgroup keeps in LDS; else -1 */
+  int32_t grid;         /* decode: workgroups; else -1 */
+  int32_t share;        /* decode: 16-row tiles of the largest workgroup share; else -1 */
+  int32_t lds_bytes;    /* decode: dynamic LDS per workgroup; else -1 */
+  int32_t tile_shape;   /* prefill: WAL_TILE_*; else -1 */
+  int32_t reserved;
+} wal_rvq_launch_info;
+
+/* What wal_rvq_linear would launch for these arguments, without launching
+ * anything (no device memory is read; x is only checked for alignment).  The
+ * environment overrides WAL2026_DECODE_XMODE (reg, lds, greg, gtr, global)
+ * and WAL2026_PREFILL_TILE (short, tall, wide) apply to both calls; a forced
+ * x-mode that does not apply to the layer makes both return WAL_EUNSUPPORTED.
+ * No reference counterpart: the reference's forward has one code path per
+ * strategy (src/runtime.py:1362-1507); this reports which of the library's
+ * kernel variants serves a call, for tests and tuning. */
+int wal_rvq_linear_info(const wal_rvq_layer* layer, int semantics, const void* x, int64_t m, int x_dtype,
+                        wal_rvq_launch_info* info);
 
 /* ---- misc ---------------------------------------------------------------- */
 

@@ -181,3 +181,104 @@ def test_linear_refuses_mismatched_image():
     rc = lib.wal_rvq_linear(ctypes.byref(L), _lib.RECONSTRUCT, 0, 0x1000, 1, _lib.BF16, None, _lib.F32, 0x2000,
                             _lib.BF16, None)
     assert rc == _lib.EINVAL and "image" in lib.wal_last_error().decode()
+
+
+def _info(L, m, x_dtype=_lib.BF16, semantics=_lib.RECONSTRUCT, x=0x8000000):
+    out = _lib.WalLaunchInfo()
+    rc = _lib.lib().wal_rvq_linear_info(ctypes.byref(L), semantics, x, m, x_dtype, ctypes.byref(out))
+    return rc, out
+
+
+def _bench_layer(rows_per_group, in_features, S, K, id_dtype, scale_rows=1):
+    L, g = _fake_layer(rows_per_group, in_features=in_features, S=S, K=K, id_dtype=id_dtype,
+                       plan=0x7000000 if len(rows_per_group) > 1 else None)
+    L.scale_rows = scale_rows
+    return L, g
+
+
+# (name, groups, in, S, K, ids, scale_rows, m, x dtype) -> (x_mode, slots, grid) on a 256-CU device
+PLANS = [
+    ("c3_down_m1", [4096], 14336, 1, 4096, _lib.I16, 128, 1, _lib.BF16, ("lds", 2, 256)),
+    ("c3_down_m2", [4096], 14336, 1, 4096, _lib.I16, 128, 2, _lib.BF16, ("lds", 1, 256)),
+    ("c3_down_m3", [4096], 14336, 1, 4096, _lib.I16, 128, 3, _lib.BF16, ("lds", 1, 256)),
+    ("c3_down_m4", [4096], 14336, 1, 4096, _lib.I16, 128, 4, _lib.BF16, ("global", 2, 256)),
+    ("c3_down_m16", [4096], 14336, 1, 4096, _lib.I16, 128, 16, _lib.BF16, ("gtr", 1, 256)),
+    ("c3_gate_up_m1", [14336, 14336], 4096, 1, 4096, _lib.I16, 128, 1, _lib.BF16, ("reg", 2, 256)),
+    ("c3_gate_up_m16", [14336, 14336], 4096, 1, 4096, _lib.I16, 128, 16, _lib.BF16, ("greg", 1, 256)),
+    ("c5_down_m1", [256] * 14, 18944, 3, 256, _lib.U8, 1, 1, _lib.BF16, ("lds", 2, 224)),
+    ("c2_down_m1", [2048], 8192, 2, 256, _lib.U8, 1, 1, _lib.BF16, ("lds", 1, 128)),
+    ("c1_m1", [2048], 2048, 2, 256, _lib.U8, 1, 1, _lib.F16, ("reg", 1, 128)),
+]
+
+
+@pytest.mark.parametrize("case", PLANS, ids=[p[0] for p in PLANS])
+def test_decode_planner_at_benchmark_shapes(case, monkeypatch):
+    """The decode launch planner's layouts at the benchmark shapes (what the
+    full-size GPU tests rely on to reach each x-mode).  No GPU is needed: the
+    query reads no device memory and assumes 256 CUs without a device."""
+    monkeypatch.delenv("WAL2026_DECODE_XMODE", raising=False)
+    _name, groups, in_f, S, K, idt, sr, m, xdt, want = case
+    L, _g = _bench_layer(groups, in_f, S, K, idt, sr)
+    rc, info = _info(L, m, xdt)
+    assert rc == _lib.OK, _lib.lib().wal_last_error()
+    assert info.kernel == _lib.KERNEL_DECODE
+    assert (_lib.XMODE_NAMES[info.x_mode], info.table_slots, info.grid) == want
+    assert info.lds_bytes <= 160 * 1024 and info.tile_shape == -1
+
+
+def test_prefill_and_generic_routing(monkeypatch):
+    monkeypatch.delenv("WAL2026_PREFILL_TILE", raising=False)
+    L, _g = _bench_layer([14336], 4096, 2, 256, _lib.U8)
+    rc, info = _info(L, 2048)
+    assert rc == _lib.OK and info.kernel == _lib.KERNEL_PREFILL and info.tile_shape == _lib.TILE_TALL
+    assert info.x_mode == -1 and info.grid == -1
+    monkeypatch.setenv("WAL2026_PREFILL_TILE", "wide")
+    rc, info = _info(L, 2048)
+    assert rc == _lib.OK and info.tile_shape == _lib.TILE_WIDE
+    # block size 32, fp32 x, a misaligned x and STAGEWISE go to the generic kernel
+    L32, _g32 = _fake_layer([64], in_features=256, block=32)
+    assert _info(L32, 1)[1].kernel == _lib.KERNEL_GENERIC
+    assert _info(L, 1, x_dtype=_lib.F32)[1].kernel == _lib.KERNEL_GENERIC
+    assert _info(L, 1, x=0x8000008)[1].kernel == _lib.KERNEL_GENERIC
+    assert _info(L, 1, semantics=_lib.STAGEWISE)[1].kernel == _lib.KERNEL_GENERIC
+    assert _info(L, 0)[1].kernel == _lib.KERNEL_NONE
+
+
+@pytest.mark.parametrize("mode", ["reg", "lds", "greg", "gtr", "global"])
+def test_forced_decode_xmode(mode, monkeypatch):
+    """WAL2026_DECODE_XMODE forces the x-mode wherever it applies; reg and
+    greg need every wave to own one 64-block chunk (B <= 512)."""
+    monkeypatch.setenv("WAL2026_DECODE_XMODE", mode)
+    small, _g = _bench_layer([256], 1024, 2, 256, _lib.U8)
+    rc, info = _info(small, 3)
+    assert rc == _lib.OK and _lib.XMODE_NAMES[info.x_mode] == mode
+    wide, _g2 = _bench_layer([256], 4608, 1, 4096, _lib.U16, 128)
+    rc, info = _info(wide, 1)
+    if mode in ("reg", "greg"):
+        assert rc == _lib.EUNSUPPORTED and "WAL2026_DECODE_XMODE" in _lib.lib().wal_last_error().decode()
+        # wal_rvq_linear refuses the same call before any launch
+        rc2 = _lib.lib().wal_rvq_linear(ctypes.byref(wide), 0, 0, 0x8000000, 1, _lib.BF16, None, _lib.F32, 0x2000,
+                                        _lib.BF16, None)
+        assert rc2 == _lib.EUNSUPPORTED
+    else:
+        assert rc == _lib.OK and _lib.XMODE_NAMES[info.x_mode] == mode
+
+
+def test_unknown_override_values_refused(monkeypatch):
+    L, _g = _bench_layer([256], 1024, 2, 256, _lib.U8)
+    monkeypatch.setenv("WAL2026_DECODE_XMODE", "fast")
+    assert _info(L, 1)[0] == _lib.EINVAL
+    monkeypatch.delenv("WAL2026_DECODE_XMODE")
+    monkeypatch.setenv("WAL2026_PREFILL_TILE", "huge")
+    assert _info(L, 64)[0] == _lib.EINVAL
+
+
+def test_decode_falls_back_when_no_layout_fits(monkeypatch):
+    """A one-stage table of 155,392 bytes (9712 entries) fits beside one
+    tile's partial sums at M = 1 but not at M = 16 (8 waves x 16 x 16 fp32
+    partials): there the call is routed to the generic kernel instead of
+    failing at launch."""
+    monkeypatch.delenv("WAL2026_DECODE_XMODE", raising=False)
+    L, _g = _bench_layer([64], 128, 1, 9712, _lib.U16)
+    assert _info(L, 1)[1].kernel == _lib.KERNEL_DECODE
+    assert _info(L, 16)[1].kernel == _lib.KERNEL_GENERIC

@@ -45,18 +45,25 @@ def test_full_weight_bitexact(name, cname, out_f, in_f, gpu_device):
     assert torch.equal(bits(got), bits(want)), name
 
 
-DECODE_CASES = [(s, m) for s in SHAPES if s[1] != "c4" for m in ((1, 4, 16) if s[1] == "c3" else (1,))]
+# (shape, m, the planner's (x-mode, table slots) there)
+DECODE_CASES = [(SHAPES[0], 1, ("reg", 2)), (SHAPES[0], 4, ("greg", 2)), (SHAPES[0], 16, ("greg", 1)),
+                (SHAPES[2], 1, ("reg", 2))]
 
 
-@pytest.mark.parametrize("shape,m", DECODE_CASES, ids=[f"{s[0]}_m{m}" for s, m in DECODE_CASES])
-def test_full_decode_parity_and_linearity(shape, m, gpu_device):
-    """M = 1, 4, 16 at c3 cover the three decode layouts the launch planner
-    picks there (x in LDS with two table slots; x from global memory into
-    registers with two slots; the same with one slot)."""
+@pytest.mark.parametrize("shape,m,plan", DECODE_CASES, ids=[f"{s[0]}_m{m}" for s, m, _ in DECODE_CASES])
+def test_full_decode_parity_and_linearity(shape, m, plan, gpu_device, monkeypatch):
+    """The gate_proj shapes (4096 or 3584 columns: every wave owns one
+    64-block chunk, so its x fragments are held in registers).  M = 1, 4, 16
+    at c3 cover the layouts the launch planner picks there: x rows staged in
+    LDS with two table slots (reg); x fragments straight from global memory
+    into registers with two slots (greg), then with one slot."""
+    monkeypatch.delenv("WAL2026_DECODE_XMODE", raising=False)
     name, cname, out_f, in_f = shape
     print(f"[fullsize] decode {name} m={m}", flush=True)
     cfg, mod, gen = _layer(cname, out_f, in_f, gpu_device)
     x = synth.make_activation(m, in_f, cfg.x_dtype, gen)
+    info = mod.launch_info(x.to(gpu_device))
+    assert (info["x_mode"], info["table_slots"]) == plan, info
     y = mod._hip_linear(x.to(gpu_device), fast=False, out_dtype=torch.float32)
     w_ref = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
     assert rel_err(y, c_oracle.linear_f64(x, w_ref)) <= TOL, name
@@ -90,20 +97,23 @@ def test_full_prefill_parity_sampled_rows(tile, gpu_device, monkeypatch):
 
 
 @pytest.mark.parametrize("m", [5, 9, 16])
-def test_full_decode_down_proj_transposed_x(m, gpu_device):
+def test_full_decode_down_proj_transposed_x(m, gpu_device, monkeypatch):
     """c3 down_proj (4096 x 14336) at 4 < M <= 16: x (up to 458 KB) fits
     neither LDS nor registers, so each item's x fragments are loaded as row
     runs and transposed through a per-wave LDS scratch, one or two 8-row
     halves (M = 5: one half; 9: a partial second half; 16: both full)."""
+    monkeypatch.delenv("WAL2026_DECODE_XMODE", raising=False)
     print(f"[fullsize] decode c3_down m={m}", flush=True)
     cfg, mod, gen = _layer("c3", 4096, 14336, gpu_device)
     x = synth.make_activation(m, 14336, cfg.x_dtype, gen)
+    assert mod.launch_info(x.to(gpu_device))["x_mode"] == "gtr"
     y = mod._hip_linear(x.to(gpu_device), fast=False, out_dtype=torch.float32)
     w_ref = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
     assert rel_err(y, c_oracle.linear_f64(x, w_ref)) <= TOL
-    # one-hot rows read the kernel's weights out exactly: columns spread over
+    # one-hot rows read the kernel's weights out exactly: a distinct column
+    # per row (rows 8-15 go through the second transpose half), spread over
     # the row, including the first and last block of a chunk
-    cols = [0, 7, 8, 511, 512, 4095, 7000, 14335][: m]
+    cols = [0, 7, 8, 511, 512, 4095, 7000, 14335, 1, 63, 64, 1023, 1024, 8191, 8192, 14329][: m]
     eye = torch.zeros(m, 14336, dtype=cfg.x_dtype)
     for i, c in enumerate(cols):
         eye[i, c] = 1.0

@@ -14,7 +14,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libwal2026_amd.so"
 
 MAX_STAGES = 8
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # wal_dtype
 U8, I16, U16, I32 = 0, 1, 2, 3
@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "wal_rvq_image_build",
     "wal_rvq_reconstruct",
     "wal_rvq_linear",
+    "wal_rvq_linear_info",
     "wal_rvq_group_linear_matmul",
     "wal_id_route_linear",
     "wal_id_route_reconstruct",
@@ -83,6 +84,28 @@ class WalLayer(ctypes.Structure):
     ]
 
 
+# wal_rvq_launch_info.kernel / x_mode / tile_shape
+KERNEL_NONE, KERNEL_DECODE, KERNEL_PREFILL, KERNEL_GENERIC = 0, 1, 2, 3
+XMODE_GLOBAL, XMODE_LDS, XMODE_REG, XMODE_GREG, XMODE_GTR = 0, 1, 2, 3, 4
+XMODE_NAMES = {XMODE_GLOBAL: "global", XMODE_LDS: "lds", XMODE_REG: "reg", XMODE_GREG: "greg", XMODE_GTR: "gtr"}
+TILE_SHORT, TILE_TALL, TILE_WIDE = 0, 1, 2
+
+
+class WalLaunchInfo(ctypes.Structure):
+    """struct wal_rvq_launch_info."""
+
+    _fields_ = [
+        ("kernel", ctypes.c_int32),
+        ("x_mode", ctypes.c_int32),
+        ("table_slots", ctypes.c_int32),
+        ("grid", ctypes.c_int32),
+        ("share", ctypes.c_int32),
+        ("lds_bytes", ctypes.c_int32),
+        ("tile_shape", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
 def image_tag(semantics: int, x_dtype_tag: int) -> int:
     """WAL_RVQ_IMAGE_TAG(semantics, x_dtype)."""
     return 0x1000 | (semantics & 0xF) | ((x_dtype_tag & 0xFF) << 4)
@@ -118,6 +141,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wal_rvq_reconstruct.argtypes = [ctypes.POINTER(WalLayer), i32, u32, vp, i32, vp]
     L.wal_rvq_linear.restype = i32
     L.wal_rvq_linear.argtypes = [ctypes.POINTER(WalLayer), i32, u32, vp, i64, i32, vp, i32, vp, i32, vp]
+    L.wal_rvq_linear_info.restype = i32
+    L.wal_rvq_linear_info.argtypes = [ctypes.POINTER(WalLayer), i32, vp, i64, i32, ctypes.POINTER(WalLaunchInfo)]
     L.wal_rvq_group_linear_matmul.restype = i32
     L.wal_rvq_group_linear_matmul.argtypes = [vp, i64, i64, i32, vp, i32, ctypes.c_int32, i64, i64, vp, i32, i64,
                                               ctypes.c_int32, vp, i32, vp, i32, vp]

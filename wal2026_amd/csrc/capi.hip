@@ -8,6 +8,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <set>
+#include <utility>
 
 #include "../../include/wal2026_amd.h"
 #include "rvq_kernels.h"
@@ -162,8 +165,8 @@ int lds_mode_for(const wal_rvq_layer& L, int sem) {
   return (L.codebook_dtype == WAL_F16 && !any_ss) ? LM_H16 : LM_F32;
 }
 
-// True when the block-size-8 MFMA kernels can run this layer.
-bool mfma_eligible(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, bool prefill) {
+// Layout conditions of the block-size-8 MFMA kernels (decode and prefill).
+bool mfma_layout_ok(const wal_rvq_layer& L, int x_dtype, const void* x) {
   if (L.block_size != 8 || (int64_t)L.blocks_per_row * 8 != L.in_features) return false;
   if (L.blocks_per_row % 16 != 0) return false;
   if (L.num_stages > 4) return false;
@@ -179,14 +182,58 @@ bool mfma_eligible(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, 
   // index and scale buffers are addressed with 32-bit buffer offsets
   for (int g = 0; g < L.n_groups; ++g)
     if ((int64_t)L.groups[g].rows * L.blocks_per_row * id_bytes(L.id_dtype) >= (int64_t)1 << 31) return false;
+  return true;
+}
+
+// The prefill kernel's table fits LDS beside its double-buffered 128 x 48 and
+// 256 x 48 16-bit tiles (8-bit ids with K < 256 get a 256-entry margin, see
+// rvq_prefill_impl.h).
+bool prefill_table_fits(const wal_rvq_layer& L, int sem) {
   const int esz = lds_mode_for(L, sem) == LM_F32 ? 32 : 16;
-  // (prefill: 8-bit ids with K < 256 get a 256-entry margin, see rvq_prefill_impl.h)
   const size_t cb = ((size_t)L.num_stages * L.codebook_size +
-                     (prefill && L.id_dtype == WAL_U8 && L.codebook_size < 256 ? 256 - L.codebook_size : 0)) * esz;
-  // prefill: double-buffered 128 x 48 and 256 x 48 16-bit tiles; decode: the
-  // partial sums of one tile from 8 waves at M = 16 and the zero row
-  const size_t budget = prefill ? (160 * 1024 - 2 * (128 + 256) * 48 * 2) : (160 * 1024 - 8 * 1024 - 256);
-  return cb <= budget;
+                     (L.id_dtype == WAL_U8 && L.codebook_size < 256 ? 256 - L.codebook_size : 0)) * esz;
+  return cb <= (size_t)(kLdsMaxBytes - 2 * (128 + 256) * 48 * 2);
+}
+
+// Which kernel serves a wal_rvq_linear call, with its launch plan.
+struct Route {
+  int kernel;     // WAL_KERNEL_*
+  DecodePlan dp;  // decode
+  int shape;      // prefill: PrefillShape
+};
+
+int route_linear(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, int64_t m, Route* r) {
+  r->kernel = WAL_KERNEL_GENERIC;
+  r->shape = -1;
+  r->dp = DecodePlan{-1, -1, -1, -1, 0};
+  if (m == 0) {
+    r->kernel = WAL_KERNEL_NONE;
+    return WAL_OK;
+  }
+  if (sem == SEM_STAGEWISE || !mfma_layout_ok(L, x_dtype, x)) return WAL_OK;
+  const int lmode = lds_mode_for(L, sem);
+  if (m <= 16) {
+    const int force = decode_xmode_override();
+    if (force == -2) return fail(WAL_EINVAL, "WAL2026_DECODE_XMODE must be reg, lds, greg, gtr or global");
+    const int esz = lmode == LM_F32 ? 32 : 16;
+    const bool segments = L.n_groups > 1 || decode_scaled_tables(L.num_stages, L.scale_rows);
+    const int n_tiles = n_tiles_of(L, 0);
+    if (plan_decode(esz, L.num_stages, L.codebook_size, (int)m, L.in_features, L.blocks_per_row, n_tiles,
+                    device_cu_count(), segments, force, &r->dp)) {
+      r->kernel = WAL_KERNEL_DECODE;
+    } else if (force >= 0) {
+      return fail(WAL_EUNSUPPORTED, "WAL2026_DECODE_XMODE forces x-mode %d, which does not apply to this layer at m = %lld",
+                  force, (long long)m);
+    }
+    return WAL_OK;
+  }
+  if (!prefill_table_fits(L, sem)) return WAL_OK;
+  const int force = prefill_tile_override();
+  if (force == -2) return fail(WAL_EINVAL, "WAL2026_PREFILL_TILE must be short, tall or wide");
+  r->kernel = WAL_KERNEL_PREFILL;
+  r->shape = plan_prefill_shape(L.num_stages, lmode, id_bytes(L.id_dtype), m, n_tiles_of(L, 2), device_cu_count(),
+                                force);
+  return WAL_OK;
 }
 
 // Resolve FAST on groups that are not "plain" (src/runtime.py:416-429, :579-580).
@@ -218,6 +265,23 @@ uint32_t resolve_mask(const wal_rvq_layer& L, uint32_t mask) {
 }
 
 }  // namespace
+
+namespace wal {
+
+hipError_t allow_max_lds(const void* kern) {
+  static std::mutex mu;
+  static std::set<std::pair<int, const void*>> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({dev, kern})) return hipSuccess;
+  e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMaxBytes);
+  if (e == hipSuccess) done.insert({dev, kern});
+  return e;
+}
+
+}  // namespace wal
 
 extern "C" {
 
@@ -344,25 +408,49 @@ int wal_rvq_linear(const wal_rvq_layer* layer, int semantics, uint32_t active_st
   // bias inside F.linear (mode 1), or added to the rounded stagewise output (mode 2, src/runtime.py:1470-1473)
   EpilogueArgs E{y, bias, (int64_t)layer->out_features, y_dtype, x_dtype, bias_dtype,
                  bias ? (sem == SEM_STAGEWISE ? 2 : 1) : 0};
-  hipError_t e;
   if (layer->image != nullptr && layer->image_tag != WAL_RVQ_IMAGE_TAG(semantics, x_dtype))
     return fail(WAL_EINVAL, "the layer's codebook image was built for tag 0x%x, this call needs 0x%x",
                 layer->image_tag, WAL_RVQ_IMAGE_TAG(semantics, x_dtype));
-  if (sem == SEM_STAGEWISE) {
-    LayerArgs A = make_args(*layer, 1, resolve_mask(*layer, 0));
-    e = launch_generic_linear(A, D, E, sem, x, m, st);
-  } else if (m <= 16 && mfma_eligible(*layer, sem, x_dtype, x, false)) {
+  Route r;
+  if ((rc = route_linear(*layer, sem, x_dtype, x, m, &r))) return rc;
+  hipError_t e;
+  if (r.kernel == WAL_KERNEL_DECODE) {
     LayerArgs A = make_args(*layer, 0, mask);
     A.image = static_cast<const uint8_t*>(layer->image);
-    e = launch_decode(A, D, E, sem, lds_mode_for(*layer, sem), x, (int)m, device_cu_count(), st);
-  } else if (m > 16 && mfma_eligible(*layer, sem, x_dtype, x, true)) {
+    e = launch_decode(A, D, E, sem, lds_mode_for(*layer, sem), x, (int)m, r.dp, st);
+  } else if (r.kernel == WAL_KERNEL_PREFILL) {
     LayerArgs A = make_args(*layer, 2, mask);
-    e = launch_prefill(A, D, E, sem, lds_mode_for(*layer, sem), x, m, device_cu_count(), st);
+    e = launch_prefill(A, D, E, sem, lds_mode_for(*layer, sem), x, m, r.shape, st);
   } else {
-    LayerArgs A = make_args(*layer, 1, mask);
+    // the generic kernel (STAGEWISE runs every stage: its mask is all stages)
+    LayerArgs A = make_args(*layer, 1, sem == SEM_STAGEWISE ? resolve_mask(*layer, 0) : mask);
     e = launch_generic_linear(A, D, E, sem, x, m, st);
   }
   return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_linear launch");
+}
+
+int wal_rvq_linear_info(const wal_rvq_layer* layer, int semantics, const void* x, int64_t m, int x_dtype,
+                        wal_rvq_launch_info* info) {
+  g_err[0] = 0;
+  if (!info) return fail(WAL_EINVAL, "info is NULL");
+  int rc = validate_layer(layer);
+  if (rc) return rc;
+  if (m < 0) return fail(WAL_EINVAL, "m must be >= 0");
+  if (!is_float_dtype(x_dtype)) return fail(WAL_EINVAL, "bad x dtype %d", x_dtype);
+  int sem = 0;
+  if ((rc = resolve_semantics(*layer, semantics, &sem))) return rc;
+  Route r;
+  if ((rc = route_linear(*layer, sem, x_dtype, x, m, &r))) return rc;
+  info->kernel = r.kernel;
+  const bool dec = r.kernel == WAL_KERNEL_DECODE;
+  info->x_mode = dec ? r.dp.xmode : -1;
+  info->table_slots = dec ? r.dp.nslots : -1;
+  info->grid = dec ? r.dp.grid : -1;
+  info->share = dec ? r.dp.share : -1;
+  info->lds_bytes = dec ? (int32_t)r.dp.lds : -1;
+  info->tile_shape = r.kernel == WAL_KERNEL_PREFILL ? r.shape : -1;
+  info->reserved = 0;
+  return WAL_OK;
 }
 
 int wal_rvq_group_linear_matmul(const void* x, int64_t m, int64_t k_in, int x_dtype, const void* stage_ids,

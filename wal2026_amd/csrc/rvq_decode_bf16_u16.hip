@@ -3,5 +3,5 @@
 
 namespace wal {
 template hipError_t decode_entry<WAL_BF16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&, int, int,
-                                              const void*, int M, int n_cu, hipStream_t);
+                                              const void*, int M, const DecodePlan&, hipStream_t);
 }  // namespace wal

@@ -39,9 +39,6 @@
 
 namespace wal {
 
-constexpr int kDecodeMaxWaves = 8;
-constexpr int kDecodeMaxThreads = kDecodeMaxWaves * 64;
-
 // Items of index loads in flight per wave.  Measured on gfx950 at every
 // benchmark shape (c2, c3, c5): one item ahead is fastest.  The loop is bound
 // by the LDS codeword gathers and the dequantisation arithmetic, not by HBM
@@ -62,21 +59,6 @@ WAL_DEVICE uint32_t extract_id(const u32x4_t (&v)[sizeof(IdT)], int t) {
   }
 }
 
-// Bytes of LDS a decode launch needs: nslots staged tables (the codebooks of
-// up to two groups / scale runs), the per-tile partial sums of every wave and
-// the output rows of every tile (max_tiles tiles per workgroup), a 256-byte
-// zero row and (xlds) the activation rows.
-constexpr int kDecodeTileMetaBytes = 16;  // {out_row0, rows, -, -} per tile
-// xscr: the per-wave x transpose scratch of XM_GTR (8 rows x 1 KB a wave).
-constexpr int kDecodeXScratchBytes = 8 * 1024;
-template <int LMODE>
-WAL_HOST_DEVICE size_t decode_lds_bytes(int S, int K, bool xlds, int M, int in, int nw, int max_tiles, int nslots,
-                                        bool xscr = false) {
-  return (size_t)nslots * S * K * lds_entry_bytes<LMODE>() +
-         (size_t)max_tiles * (nw * M * 16 * sizeof(float) + kDecodeTileMetaBytes) + 256 +
-         (xlds ? (size_t)M * in * sizeof(uint16_t) : 0) + (xscr ? (size_t)nw * kDecodeXScratchBytes : 0);
-}
-
 // Tile metadata through the scalar cache (uniform t): no vector-memory
 // instruction, so reading it never waits on the index loads in flight.
 template <int S>
@@ -92,7 +74,6 @@ WAL_DEVICE FragTile<S> tile_at(const LayerArgs& L, int t) {
     f.p.stage_scales = L.g0.stage_scales;
     f.group = 0;
     f.row0 = t * 16;
-    f.rows = min(16, L.g0.rows - f.row0);
     f.out_row0 = L.g0.row0 + f.row0;
     f.grows = L.g0.rows;
   } else {
@@ -109,11 +90,18 @@ WAL_DEVICE FragTile<S> tile_at(const LayerArgs& L, int t) {
     f.p.stage_scales = G->stage_scales;
     f.group = pt->group;
     f.row0 = pt->row0;
-    f.rows = pt->rows;
     f.out_row0 = pt->out_row0;
     f.grows = G->rows;
   }
   return f;
+}
+
+// Rows of a decode tile: its 16-row slice of the group, shorter at the
+// group's end.  (Derived, not kept in the tile: a field that only some paths
+// update makes the compiler keep the tile in scratch memory.)
+template <int S>
+WAL_DEVICE int tile_rows(const FragTile<S>& f) {
+  return min(16, f.grows - f.row0);
 }
 
 // Tile t + 1 from tile t (f).  A group's tiles are consecutive 16-row tiles
@@ -127,7 +115,6 @@ WAL_DEVICE FragTile<S> next_tile(const LayerArgs& L, const FragTile<S>& f, int t
     FragTile<S> n = f;
     n.row0 += 16;
     n.out_row0 += 16;
-    n.rows = min(16, n.grows - n.row0);
     return n;
   }
   return tile_at<S>(L, t_next);
@@ -142,36 +129,18 @@ WAL_DEVICE int table_key(const LayerArgs& L, const FragTile<S>& f) {
 WAL_DEVICE float scale_bits_to_f32(uint32_t h, int dt) { return dt == WAL_F16 ? f16_to_f32(h) : bf16_to_f32(h); }
 
 // Stage one table (a group's codebooks, scaled by rs for SCALE_TABLE) from
-// the image when there is one, else from the raw codebooks.  Out of line: the
-// rare paths that call it (restaging in the loop, a launch without an image)
-// then cost one copy of this code instead of one per unrolled pipeline slot;
-// the kernels are small enough to stay in the instruction cache.
-//
-// The destination is an offset into the dynamic LDS (decode_smem), so the
-// stores stay LDS stores inside the out-of-line function.
+// the image when there is one, else from the raw codebooks.  Inlined: an
+// out-of-line call would give the kernel a call frame and a private (scratch)
+// segment that every launch has to set up.
 extern __shared__ __attribute__((aligned(16))) uint8_t decode_smem[];
 
 template <int S, int LMODE, int SEM, int XDT, bool SCALE_TABLE>
-__device__ __attribute__((noinline)) void stage_table(uint32_t dst_off, const uint8_t* img, GroupPtrs<S> p, int K,
-                                                      DtypeArgs D, RowScale rs) {
+WAL_DEVICE void stage_table(uint32_t dst_off, const uint8_t* img, const GroupPtrs<S>& p, int K, const DtypeArgs& D,
+                            const RowScale& rs) {
   uint8_t* dst = decode_smem + dst_off;
   if (img != nullptr) stage_image<XDT, SCALE_TABLE>(dst, img, S * K * lds_entry_bytes<LMODE>() / 16, rs);
   else stage_codebooks<S, LMODE, SEM, XDT, SCALE_TABLE>(dst, p, K, D, rs);
 }
-
-// Where the MFMA's activation fragments come from.
-enum XMode : int {
-  XM_GLOBAL = 0,  // x does not fit in LDS: read per item from global memory (L2)
-  XM_LDS = 1,     // x staged in LDS, fragments read per item
-  XM_REG = 2,     // x staged in LDS; each wave owns one chunk (CPT == 1), so its
-                  // 16 fragments are read once and kept in registers
-  XM_GREG = 3,    // as XM_REG, but the 16 fragments come straight from global
-                  // memory (large M: x beside two tables would not fit LDS)
-  XM_GTR = 4      // M > 4, x too large for LDS: per item, each load reads one
-                  // contiguous 1 KB run of an x row and the fragments are
-                  // transposed through a per-wave LDS scratch (XM_GLOBAL's
-                  // direct fragment loads touch 64 cache lines each)
-};
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int XMODE, bool SCALED>
 __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
@@ -217,9 +186,10 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   const int t_end = t_begin + n_tiles_wg;
   const int n_items = n_tiles_wg * CPT;
   const int xm = min(nl, M - 1);  // x row this lane feeds to the MFMA
-  // Index mask: ids are validated against K on the host; the mask keeps any
-  // other value inside the LDS allocation (next power of two of K entries).
-  const uint32_t kmask = K <= 1 ? 0u : (0xffffffffu >> __builtin_clz((uint32_t)(K - 1)));
+  // Ids are validated against K by the caller; one past the range is clamped
+  // to the last entry, as every kernel of the library does, so it never reads
+  // outside the staged table.
+  const uint32_t kmax = (uint32_t)(K - 1);
 
   // ---- prologue, part 1: loads of the activations and tables ---------------
   // The range's tiles fall in one or two table segments (same group and, for
@@ -245,12 +215,13 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
       const int dr = (seg1 - t_begin) * 16;
       sti.row0 += dr;
       sti.out_row0 += dr;
-      sti.rows = min(16, sti.grows - sti.row0);
     } else {
       sti = tile_at<S>(L, seg1);
     }
   }
-  int key[2] = {table_key<S, SCALED>(L, cti), two ? table_key<S, SCALED>(L, sti) : -1};
+  // keys of the tables in slots 0 and 1 (two scalars: a dynamically indexed
+  // array would live in scratch memory)
+  int key0 = table_key<S, SCALED>(L, cti), key1 = two ? table_key<S, SCALED>(L, sti) : -1;
   const bool have_image = L.image != nullptr;
   const uint8_t* img0 = have_image ? L.image + (size_t)cti.group * tbl_bytes : nullptr;
   const uint8_t* img1 = have_image ? L.image + (size_t)sti.group * tbl_bytes : nullptr;
@@ -314,7 +285,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
     const int c = wave + NW * is_c;
     const bool ok = is_t < n_tiles_wg && c < nchunk;  // uniform
     const int base = min(c * 64 + 16 * q, B - 16);
-    const int r = iti.row0 + min(nl, iti.rows - 1);
+    const int r = iti.row0 + min(nl, tile_rows<S>(iti) - 1);
     const uint32_t off = ok ? (uint32_t)((r * B + base) * (int)sizeof(IdT)) : kBufOOB;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -408,11 +379,11 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
         // first item of a tile: pick its table slot
         if (ct_t > 0) cti = next_tile<S>(L, cti, t_begin + ct_t);  // tile t_begin: the prologue's
         // the epilogue's output rows of this tile (no plan read there)
-        if (tid == 0) reinterpret_cast<int2*>(tmeta)[2 * ct_t] = make_int2(cti.out_row0, cti.rows);
+        if (tid == 0) reinterpret_cast<int2*>(tmeta)[2 * ct_t] = make_int2(cti.out_row0, tile_rows<S>(cti));
         const int k = table_key<S, SCALED>(L, cti);
-        if (k == key[0]) {
+        if (k == key0) {
           slot = 0;
-        } else if (k == key[1]) {
+        } else if (k == key1) {
           slot = 1;
         } else {
           // a segment no slot holds: restage into the slot the previous tile
@@ -425,7 +396,8 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
                                                   L.image != nullptr ? L.image + (size_t)cti.group * tbl_bytes : nullptr,
                                                   cti.p, K, D, r);
           __syncthreads();
-          key[slot] = k;
+          if (slot == 0) key0 = k;
+          else key1 = k;
         }
         if constexpr (!SCALED) rs = make_row_scale<XDT>(scale_bits_to_f32(rsr[j], D.sc_dtype));
         acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -465,7 +437,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
         for (int tt = 0; tt < 16; ++tt) {
           uint32_t id[S];
 #pragma unroll
-          for (int s = 0; s < S; ++s) id[s] = extract_id<IdT>(cur[s], tt) & kmask;
+          for (int s = 0; s < S; ++s) id[s] = min(extract_id<IdT>(cur[s], tt), kmax);
           if constexpr (SCALED) wf[tt] = *reinterpret_cast<const u32x4_t*>(tbl + (size_t)id[0] * 16);
           else wf[tt] = make_wfrag<S, LMODE, SEM, XDT>(tbl, id, K, L.active_mask, rs);
         }
@@ -541,89 +513,36 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT, bool SCALED>
 static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x, int M,
-                            int n_cu, hipStream_t st) {
-  constexpr int kLdsMax = 160 * 1024;
-  const int nw = kDecodeMaxWaves;
-  const int S_ = S, K = L.codebook_size, in = L.in_features;
-  // Each workgroup takes an equal share of the tiles and keeps the partial
-  // sums of its whole share in LDS; when a share does not fit, the grid grows
-  // until it does.
-  auto plan_for = [&](int nslots, bool xlds, bool xscr, int* grid, int* share) -> bool {
-    const size_t fixed = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, 0, nslots, xscr);
-    const size_t per_tile = (size_t)nw * M * 16 * sizeof(float) + kDecodeTileMetaBytes;
-    if (fixed + per_tile > (size_t)kLdsMax) return false;
-    const int fit = (int)(((size_t)kLdsMax - fixed) / per_tile);
-    int g = n_cu < L.n_tiles ? n_cu : L.n_tiles;
-    const int min_grid = (L.n_tiles + fit - 1) / fit;
-    if (g < min_grid) g = min_grid;
-    *grid = g;
-    *share = (L.n_tiles + g - 1) / g;
-    return true;
-  };
-  // Candidate layouts in order of preference; the first whose grid fits one
-  // round of workgroups (one per CU) wins, else the one with the fewest
-  // rounds.  Two table slots when a workgroup's tiles can span two tables
-  // (several groups, or scaled tables with more than one scale run); x in
-  // LDS, or in registers straight from global memory when each wave owns one
-  // chunk (large M, where x beside the tables would not fit), or read per
-  // item from global memory.
-  const bool segments = L.plan != nullptr || SCALED;
-  const int nchunk = (L.blocks_per_row + 63) / 64;
-  const bool one_chunk = nchunk <= nw;
-  struct Cand { int xmode, nslots; };
-  const Cand cands[] = {{one_chunk ? XM_REG : XM_LDS, 2}, {XM_GREG, 2}, {one_chunk ? XM_REG : XM_LDS, 1},
-                        {XM_GREG, 1}, {XM_GTR, 2}, {XM_GTR, 1}, {XM_GLOBAL, 2}, {XM_GLOBAL, 1}};
-  int grid = 0, share = 1, nslots = 0, xmode = XM_GLOBAL, best_rounds = 1 << 30;
-  for (const Cand& c : cands) {
-    if (c.nslots == 2 && !segments) continue;
-    if (c.xmode == XM_GREG && !one_chunk) continue;
-    if (c.xmode == XM_GTR && M <= 4) continue;  // up to 4 rows, direct loads touch at most 16 lines
-    int g = 0, sh = 1;
-    if (!plan_for(c.nslots, c.xmode == XM_REG || c.xmode == XM_LDS, c.xmode == XM_GTR, &g, &sh)) continue;
-    const int rounds = (g + n_cu - 1) / n_cu;
-    if (rounds < best_rounds) {
-      best_rounds = rounds;
-      grid = g; share = sh; nslots = c.nslots; xmode = c.xmode;
-    }
-    if (rounds <= 1) break;
-  }
-  if (nslots == 0) return hipErrorInvalidValue;  // excluded by the host's eligibility check
-  const bool xlds = xmode == XM_REG || xmode == XM_LDS;
-  const size_t lds = decode_lds_bytes<LMODE>(S_, K, xlds, M, in, nw, share, nslots, xmode == XM_GTR);
-  if (grid < 1) return hipSuccess;
-  auto kern = xmode == XM_REG    ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_REG, SCALED>
-              : xmode == XM_LDS  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_LDS, SCALED>
-              : xmode == XM_GREG ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GREG, SCALED>
-              : xmode == XM_GTR  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GTR, SCALED>
-                                 : rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GLOBAL, SCALED>;
-  static bool attr_set[5] = {false, false, false, false, false};
-  if (!attr_set[xmode]) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       kLdsMax);
-    if (e != hipSuccess) return e;
-    attr_set[xmode] = true;
-  }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(nw * 64), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M,
-                     share, nslots);
+                            const DecodePlan& P, hipStream_t st) {
+  if (P.grid < 1) return hipSuccess;
+  auto kern = P.xmode == XM_REG    ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_REG, SCALED>
+              : P.xmode == XM_LDS  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_LDS, SCALED>
+              : P.xmode == XM_GREG ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GREG, SCALED>
+              : P.xmode == XM_GTR  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GTR, SCALED>
+                                   : rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GLOBAL, SCALED>;
+  hipError_t e = allow_max_lds(reinterpret_cast<const void*>(kern));
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(P.grid), dim3(kDecodeMaxThreads), P.lds, st, L, D, E,
+                     reinterpret_cast<const uint16_t*>(x), M, P.share, P.nslots);
   return hipGetLastError();
 }
 
 template <int S, typename IdT, int XDT>
 static hipError_t decode_sem(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                             const void* x, int M, int n_cu, hipStream_t st) {
+                             const void* x, int M, const DecodePlan& P, hipStream_t st) {
   if constexpr (S == 1) {
-    // one stage: the row-scale product can be folded into the staged table
-    // when every 16-row tile has a single scale value
-    const bool scaled = L.scale_rows >= 16 && (L.scale_rows & (L.scale_rows - 1)) == 0;
+    // one stage: the row-scale product is folded into the staged table when
+    // every 16-row tile has a single scale value (decode_scaled_tables)
+    const bool scaled = decode_scaled_tables(L.num_stages, L.scale_rows);
     if (sem == SEM_FAST)
-      return scaled ? decode_go<S, IdT, LM_A16, SEM_FAST, XDT, true>(L, D, E, x, M, n_cu, st)
-                    : decode_go<S, IdT, LM_A16, SEM_FAST, XDT, false>(L, D, E, x, M, n_cu, st);
-    return scaled ? decode_go<S, IdT, LM_A16, SEM_RECON, XDT, true>(L, D, E, x, M, n_cu, st)
-                  : decode_go<S, IdT, LM_A16, SEM_RECON, XDT, false>(L, D, E, x, M, n_cu, st);
+      return scaled ? decode_go<S, IdT, LM_A16, SEM_FAST, XDT, true>(L, D, E, x, M, P, st)
+                    : decode_go<S, IdT, LM_A16, SEM_FAST, XDT, false>(L, D, E, x, M, P, st);
+    return scaled ? decode_go<S, IdT, LM_A16, SEM_RECON, XDT, true>(L, D, E, x, M, P, st)
+                  : decode_go<S, IdT, LM_A16, SEM_RECON, XDT, false>(L, D, E, x, M, P, st);
   } else {
-    if (sem == SEM_FAST) return decode_go<S, IdT, LM_A16, SEM_FAST, XDT, false>(L, D, E, x, M, n_cu, st);
-    if (lmode == LM_H16) return decode_go<S, IdT, LM_H16, SEM_RECON, XDT, false>(L, D, E, x, M, n_cu, st);
-    return decode_go<S, IdT, LM_F32, SEM_RECON, XDT, false>(L, D, E, x, M, n_cu, st);
+    if (sem == SEM_FAST) return decode_go<S, IdT, LM_A16, SEM_FAST, XDT, false>(L, D, E, x, M, P, st);
+    if (lmode == LM_H16) return decode_go<S, IdT, LM_H16, SEM_RECON, XDT, false>(L, D, E, x, M, P, st);
+    return decode_go<S, IdT, LM_F32, SEM_RECON, XDT, false>(L, D, E, x, M, P, st);
   }
 }
 
@@ -631,12 +550,12 @@ static hipError_t decode_sem(const LayerArgs& L, const DtypeArgs& D, const Epilo
 // rvq_decode_<x>_<ids>.hip so the variants compile in parallel.
 template <int XDT, typename IdT>
 hipError_t decode_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                        const void* x, int M, int n_cu, hipStream_t st) {
+                        const void* x, int M, const DecodePlan& P, hipStream_t st) {
   switch (L.num_stages) {
-    case 1: return decode_sem<1, IdT, XDT>(L, D, E, sem, lmode, x, M, n_cu, st);
-    case 2: return decode_sem<2, IdT, XDT>(L, D, E, sem, lmode, x, M, n_cu, st);
-    case 3: return decode_sem<3, IdT, XDT>(L, D, E, sem, lmode, x, M, n_cu, st);
-    default: return decode_sem<4, IdT, XDT>(L, D, E, sem, lmode, x, M, n_cu, st);
+    case 1: return decode_sem<1, IdT, XDT>(L, D, E, sem, lmode, x, M, P, st);
+    case 2: return decode_sem<2, IdT, XDT>(L, D, E, sem, lmode, x, M, P, st);
+    case 3: return decode_sem<3, IdT, XDT>(L, D, E, sem, lmode, x, M, P, st);
+    default: return decode_sem<4, IdT, XDT>(L, D, E, sem, lmode, x, M, P, st);
   }
 }
 

@@ -2,6 +2,7 @@
 #pragma once
 
 #include "rvq_common.h"
+#include "rvq_plan.h"
 
 namespace wal {
 
@@ -67,32 +68,43 @@ enum LdsMode : int { LM_A16 = 0, LM_H16 = 1, LM_F32 = 2 };
 // Codebook image of every group in LdsMode form (rvq_generic.hip).
 hipError_t launch_image(const LayerArgs& L, const DtypeArgs& D, int sem, int lmode, void* dst, hipStream_t st);
 
+// Let kernel `kern` use the whole 160 KB of LDS (hipFuncSetAttribute), once
+// per kernel and device; thread-safe (capi.hip).
+hipError_t allow_max_lds(const void* kern);
+
+// One-stage decode launches fold the row scale into the staged codebook when
+// every 16-row tile has a single scale value (scale runs of a power of two
+// >= 16 rows).
+inline __host__ __device__ bool decode_scaled_tables(int num_stages, int scale_rows) {
+  return num_stages == 1 && scale_rows >= 16 && (scale_rows & (scale_rows - 1)) == 0;
+}
+
 template <int XDT, typename IdT>
 hipError_t decode_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                        const void* x, int M, int n_cu, hipStream_t st);
+                        const void* x, int M, const DecodePlan& P, hipStream_t st);
 template <int XDT, typename IdT>
 hipError_t prefill_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                         const void* x, int64_t M, int n_cu, hipStream_t st);
+                         const void* x, int64_t M, int shape, hipStream_t st);
 
 // One explicit instantiation per (activation dtype, index width), each in its
 // own translation unit (rvq_decode_<x>_<ids>.hip, rvq_prefill_<x>_<ids>.hip);
 // these declarations keep every other unit from instantiating them again.
 extern template hipError_t decode_entry<WAL_BF16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                           int, int, const void*, int, int, hipStream_t);
+    int, int, const void*, int, const DecodePlan&, hipStream_t);
 extern template hipError_t decode_entry<WAL_BF16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                            int, int, const void*, int, int, hipStream_t);
+    int, int, const void*, int, const DecodePlan&, hipStream_t);
 extern template hipError_t decode_entry<WAL_F16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                          int, int, const void*, int, int, hipStream_t);
+    int, int, const void*, int, const DecodePlan&, hipStream_t);
 extern template hipError_t decode_entry<WAL_F16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                           int, int, const void*, int, int, hipStream_t);
+    int, int, const void*, int, const DecodePlan&, hipStream_t);
 extern template hipError_t prefill_entry<WAL_BF16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                            int, int, const void*, int64_t, int, hipStream_t);
+    int, int, const void*, int64_t, int, hipStream_t);
 extern template hipError_t prefill_entry<WAL_BF16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                             int, int, const void*, int64_t, int, hipStream_t);
+    int, int, const void*, int64_t, int, hipStream_t);
 extern template hipError_t prefill_entry<WAL_F16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                           int, int, const void*, int64_t, int, hipStream_t);
+    int, int, const void*, int64_t, int, hipStream_t);
 extern template hipError_t prefill_entry<WAL_F16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-                                                            int, int, const void*, int64_t, int, hipStream_t);
+    int, int, const void*, int64_t, int, hipStream_t);
 
 // Nearest codeword of n blocks of d floats (d in {1, 2, 4, 8, 16, 32}),
 // rvq_assign.hip.
@@ -104,25 +116,26 @@ hipError_t launch_centroid_sums(const int64_t* ids, int64_t n, const float* bloc
                                 int64_t* counts, hipStream_t st);
 
 inline hipError_t launch_decode(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
-                                int lds_mode, const void* x, int M, int n_cu, hipStream_t st) {
+                                int lds_mode, const void* x, int M, const DecodePlan& P, hipStream_t st) {
   if (L.n_tiles == 0) return hipSuccess;
   const bool wide = D.id_dtype != WAL_U8;
   if (D.x_dtype == WAL_BF16)
-    return wide ? decode_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, n_cu, st)
-                : decode_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, n_cu, st);
-  return wide ? decode_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, n_cu, st)
-              : decode_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, n_cu, st);
+    return wide ? decode_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, P, st)
+                : decode_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, P, st);
+  return wide ? decode_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, P, st)
+              : decode_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, P, st);
 }
 
+// shape: PrefillShape from plan_prefill_shape.
 inline hipError_t launch_prefill(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
-                                 int lds_mode, const void* x, int64_t M, int n_cu, hipStream_t st) {
+                                 int lds_mode, const void* x, int64_t M, int shape, hipStream_t st) {
   if (L.n_tiles == 0 || M == 0) return hipSuccess;
   const bool wide = D.id_dtype != WAL_U8;
   if (D.x_dtype == WAL_BF16)
-    return wide ? prefill_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, n_cu, st)
-                : prefill_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, n_cu, st);
-  return wide ? prefill_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, n_cu, st)
-              : prefill_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, n_cu, st);
+    return wide ? prefill_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, shape, st)
+                : prefill_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, shape, st);
+  return wide ? prefill_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, shape, st)
+              : prefill_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, shape, st);
 }
 
 }  // namespace wal

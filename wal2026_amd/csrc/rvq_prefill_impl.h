@@ -301,7 +301,7 @@ WAL_HOST_DEVICE size_t prefill_tall_lds_bytes(int K, int rshift) {
 // the compiler's resource report: no scratch).
 template <int S, typename IdT, int LMODE>
 constexpr bool tall_supported() {
-  return S <= 2 && LMODE != LM_F32;
+  return prefill_tall_ok(S, LMODE);
 }
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT>
@@ -485,13 +485,8 @@ static hipError_t prefill_tall(const LayerArgs& L, const DtypeArgs& D, const Epi
     --rshift;
   const size_t lds = prefill_tall_lds_bytes<S, IdT, LMODE>(L.codebook_size, rshift);
   auto kern = rvq_prefill_tall_kernel<S, IdT, LMODE, SEM, XDT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = allow_max_lds(reinterpret_cast<const void*>(kern));
+  if (e != hipSuccess) return e;
   const int n_mt = (int)((M + TBM - 1) / TBM);
   dim3 grid((unsigned)(L.n_tiles * (int64_t)n_mt));
   hipLaunchKernelGGL(kern, grid, dim3(kTallThreads), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M, n_mt,
@@ -527,7 +522,7 @@ WAL_HOST_DEVICE size_t prefill_wide_lds_bytes(int K, int rshift) {
 // resource report).
 template <int S, typename IdT, int LMODE>
 constexpr bool wide_supported() {
-  return !(S >= 4 && LMODE == LM_F32 && sizeof(IdT) == 2);
+  return prefill_wide_ok(S, LMODE, (int)sizeof(IdT));
 }
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT>
@@ -703,13 +698,8 @@ static hipError_t prefill_wide(const LayerArgs& L, const DtypeArgs& D, const Epi
     --rshift;
   const size_t lds = prefill_wide_lds_bytes<S, IdT, LMODE>(L.codebook_size, rshift);
   auto kern = rvq_prefill_wide_kernel<S, IdT, LMODE, SEM, XDT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = allow_max_lds(reinterpret_cast<const void*>(kern));
+  if (e != hipSuccess) return e;
   const int n_mt = (int)((M + TBM - 1) / TBM);
   dim3 grid((unsigned)(L.n_tiles * (int64_t)2 * n_mt));
   hipLaunchKernelGGL(kern, grid, dim3(kWideThreads), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M, n_mt,
@@ -729,13 +719,8 @@ static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const Epilo
     --rshift;
   const size_t lds = prefill_lds_bytes<S, IdT, LMODE>(TM, L.codebook_size, rshift);
   auto kern = rvq_prefill_kernel<S, IdT, LMODE, SEM, XDT, TM>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = allow_max_lds(reinterpret_cast<const void*>(kern));
+  if (e != hipSuccess) return e;
   const int n_mt = (int)((M + prefill_bm<TM>() - 1) / prefill_bm<TM>());
   dim3 grid((unsigned)(L.n_tiles * (int64_t)n_mt));
   hipLaunchKernelGGL(kern, grid, dim3(kPrefillThreads), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M,
@@ -743,50 +728,29 @@ static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const Epilo
   return hipGetLastError();
 }
 
-// One tile shape: 128 x-rows x 256 weight rows (TM = 4, a 64 x 64 tile per
-// wave).  A 256-row x tile (TM = 8) would halve the LDS operand reads per MFMA
-// but needs 128 accumulator registers per lane on top of the pipeline's ~100,
-// more than the 256 a lane has at two waves per SIMD.
+// shape: the tile shape from plan_prefill_shape (PS_SHORT when the instance
+// has no kernel of the requested shape).  Short is 128 x-rows x 256 weight
+// rows (TM = 4, a 64 x 64 tile per wave).
 template <int S, typename IdT, int LMODE, int SEM, int XDT>
 static hipError_t prefill_go(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
-                             int64_t M, int n_cu, hipStream_t st) {
-  // WAL2026_PREFILL_TILE=short|tall|wide forces a tile shape (tests, tuning).
-  const char* force = getenv("WAL2026_PREFILL_TILE");
+                             int64_t M, int shape, hipStream_t st) {
   constexpr bool can_tall = tall_supported<S, IdT, LMODE>(), can_wide = wide_supported<S, IdT, LMODE>();
-  int shape = 0;  // 0 short, 1 tall, 2 wide
-  if (force != nullptr && strcmp(force, "short") == 0) {
-    shape = 0;
-  } else if (force != nullptr && strcmp(force, "tall") == 0) {
-    shape = can_tall ? 1 : 0;
-  } else if (force != nullptr && strcmp(force, "wide") == 0) {
-    shape = can_wide ? 2 : 0;
-  } else if (M > 128) {
-    // One workgroup per CU, and every shape's workgroup runs the same k-steps:
-    // cost = rounds of workgroups x time per k-step, measured at c4 (gfx950)
-    // as 0.84 (short), 1.22 (tall), 0.76 (wide) us.
-    const int64_t cu = n_cu > 0 ? n_cu : 256;
-    const int64_t mt256 = (M + TBM - 1) / TBM;
-    const int64_t c_short = (L.n_tiles * ((M + 127) / 128) + cu - 1) / cu * 84;
-    const int64_t c_tall = can_tall ? (L.n_tiles * mt256 + cu - 1) / cu * 122 : INT64_MAX;
-    const int64_t c_wide = can_wide ? (L.n_tiles * 2 * mt256 + cu - 1) / cu * 76 : INT64_MAX;
-    shape = c_tall <= c_wide && c_tall < c_short ? 1 : (c_wide < c_short ? 2 : 0);
-  }
   if constexpr (can_tall)
-    if (shape == 1) return prefill_tall<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
+    if (shape == PS_TALL) return prefill_tall<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
   if constexpr (can_wide)
-    if (shape == 2) return prefill_wide<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
+    if (shape == PS_WIDE) return prefill_wide<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
   return prefill_tm<S, IdT, LMODE, SEM, XDT, 4>(L, D, E, x, M, st);
 }
 
 template <int S, typename IdT, int XDT>
 static hipError_t prefill_sem(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                              const void* x, int64_t M, int n_cu, hipStream_t st) {
-  if (sem == SEM_FAST) return prefill_go<S, IdT, LM_A16, SEM_FAST, XDT>(L, D, E, x, M, n_cu, st);
+                              const void* x, int64_t M, int shape, hipStream_t st) {
+  if (sem == SEM_FAST) return prefill_go<S, IdT, LM_A16, SEM_FAST, XDT>(L, D, E, x, M, shape, st);
   if constexpr (S == 1) {
-    return prefill_go<S, IdT, LM_A16, SEM_RECON, XDT>(L, D, E, x, M, n_cu, st);
+    return prefill_go<S, IdT, LM_A16, SEM_RECON, XDT>(L, D, E, x, M, shape, st);
   } else {
-    if (lmode == LM_H16) return prefill_go<S, IdT, LM_H16, SEM_RECON, XDT>(L, D, E, x, M, n_cu, st);
-    return prefill_go<S, IdT, LM_F32, SEM_RECON, XDT>(L, D, E, x, M, n_cu, st);
+    if (lmode == LM_H16) return prefill_go<S, IdT, LM_H16, SEM_RECON, XDT>(L, D, E, x, M, shape, st);
+    return prefill_go<S, IdT, LM_F32, SEM_RECON, XDT>(L, D, E, x, M, shape, st);
   }
 }
 
@@ -794,12 +758,12 @@ static hipError_t prefill_sem(const LayerArgs& L, const DtypeArgs& D, const Epil
 // rvq_prefill_<x>_<ids>.hip.
 template <int XDT, typename IdT>
 hipError_t prefill_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                         const void* x, int64_t M, int n_cu, hipStream_t st) {
+                         const void* x, int64_t M, int shape, hipStream_t st) {
   switch (L.num_stages) {
-    case 1: return prefill_sem<1, IdT, XDT>(L, D, E, sem, lmode, x, M, n_cu, st);
-    case 2: return prefill_sem<2, IdT, XDT>(L, D, E, sem, lmode, x, M, n_cu, st);
-    case 3: return prefill_sem<3, IdT, XDT>(L, D, E, sem, lmode, x, M, n_cu, st);
-    default: return prefill_sem<4, IdT, XDT>(L, D, E, sem, lmode, x, M, n_cu, st);
+    case 1: return prefill_sem<1, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, st);
+    case 2: return prefill_sem<2, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, st);
+    case 3: return prefill_sem<3, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, st);
+    default: return prefill_sem<4, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, st);
   }
 }
 

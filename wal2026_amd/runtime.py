@@ -225,6 +225,27 @@ def _scale_runs(groups, row_slices) -> tuple[int, list[Tensor] | None]:
     return 1, None
 
 
+_KERNEL_NAMES = {_lib.KERNEL_NONE: "none", _lib.KERNEL_DECODE: "decode", _lib.KERNEL_PREFILL: "prefill",
+                 _lib.KERNEL_GENERIC: "generic"}
+_TILE_NAMES = {_lib.TILE_SHORT: "short", _lib.TILE_TALL: "tall", _lib.TILE_WIDE: "wide"}
+
+
+def _launch_info(layer: "_lib.WalLayer", semantics: int, x: Tensor) -> dict:
+    """wal_rvq_linear_info for a call of ``layer`` on activations x (2-D view
+    of ``x``; only its shape, dtype and alignment are read)."""
+    x_flat = x.reshape(-1, x.shape[-1])
+    info = _lib.WalLaunchInfo()
+    _lib.check(_lib.lib().wal_rvq_linear_info(ctypes.byref(layer), semantics, x_flat.data_ptr(), x_flat.shape[0],
+                                              _lib.float_tag(x_flat.dtype), ctypes.byref(info)))
+    out = {"kernel": _KERNEL_NAMES[info.kernel]}
+    if info.kernel == _lib.KERNEL_DECODE:
+        out.update(x_mode=_lib.XMODE_NAMES[info.x_mode], table_slots=info.table_slots, grid=info.grid,
+                   share=info.share, lds_bytes=info.lds_bytes)
+    elif info.kernel == _lib.KERNEL_PREFILL:
+        out["tile_shape"] = _TILE_NAMES[info.tile_shape]
+    return out
+
+
 def _desc_key(groups) -> tuple:
     g0 = groups[0]
     return (g0.row_scale.data_ptr(), getattr(g0, "stage_ids_0").data_ptr(), len(groups),
@@ -517,6 +538,15 @@ class PackedGroupedBlockRVQLinear(nn.Module):
                                                   out.data_ptr(), _lib.float_tag(out_dtype), _lib.stream_ptr(dev)))
         return out
 
+    def launch_info(self, x: Tensor, fast: bool | None = None) -> dict:
+        """Which kernel variant forward(x) launches (wal_rvq_linear_info):
+        ``kernel`` ("decode", "prefill", "generic" or "none") and, for decode,
+        ``x_mode`` / ``table_slots`` / ``grid`` / ``share`` / ``lds_bytes``,
+        for prefill ``tile_shape``.  Nothing is launched."""
+        if fast is None:
+            fast = self.matmul_strategy in _FAST_STRATEGIES
+        return _launch_info(self._descriptor().layer, _lib.RECONSTRUCT_FAST if fast else _lib.RECONSTRUCT, x)
+
     # -- forward -------------------------------------------------------------
     def _hip_linear(self, x_flat: Tensor, fast: bool, out_dtype: torch.dtype | None = None) -> Tensor:
         dev = _lib.require_rocm(x_flat, self.groups[0].row_scale)
@@ -656,6 +686,11 @@ class FusedBlockRVQLinears(nn.Module):
     def invalidate_caches(self) -> None:
         self._desc = None
         self._bias = None
+
+    def launch_info(self, x: Tensor) -> dict:
+        """Which kernel variant forward(x) launches (see
+        PackedGroupedBlockRVQLinear.launch_info)."""
+        return _launch_info(self._descriptor().layer, _lib.RECONSTRUCT_FAST if self._fast else _lib.RECONSTRUCT, x)
 
     def forward(self, x: Tensor) -> tuple[Tensor, ...]:
         orig = x.shape
