@@ -9,6 +9,13 @@ derivation is in the comment beside it.
 
 reconstruct_golden.json: block_size 1, one row, codebook entry i is used by
 column i; each case is W[0, i] = rne(rne(sum_s c_s[i]) * rne(s)).
+
+route_golden.json: the scalar route-codebook weight of one (codebook_sum,
+row_scale) pair in both of the reference's roundings:
+  mode 0, PackedIDRouteLinear (src/runtime.py:89-97): the product in the
+    buffers' dtype, then cast to x dtype: rne_x(rne_buf(cs * rs));
+  mode 1, id_route_linear_matmul (src/triton_id_matmul.py:59-60): each
+    operand cast to x dtype, product in x dtype: rne_x(rne_x(cs) * rne_x(rs)).
 """
 from __future__ import annotations
 
@@ -94,6 +101,44 @@ CASES = [
     },
 ]
 
+BF16 = {
+    "1+2^-7": 0x3F81,       # bf16 1 + 2^-7 (fraction 1 of 7 bits)
+    "1+2^-3": 0x3F90,       # 1 + 2^-3 (fraction 0x10)
+}
+
+# (name, buffer dtype, x dtype, codebook_sum bits, row_scale bits, mode 0 bits, mode 1 bits)
+ROUTE = [
+    ("bf16x_double_rounding", "f16", "bf16", 0x3C05, 0x3BFF, 0x3F80, 0x3F81),
+    # cs = 1 + 2^-8 + 2^-10 (fp16 fraction 5), rs = 1 - 2^-11 (fp16 0x3BFF = 2^-1 * (2 - 2^-10)).
+    # mode 0: cs*rs = 1 + 2^-8 + 2^-11 - 2^-19 - 2^-21, just below 1 + 2^-8 + 2^-11 (half an fp16 ulp
+    #   2^-10 above 1 + 2^-8) -> fp16 1 + 2^-8 (0x3C04); that is a bf16 tie (half of 2^-7) whose even
+    #   neighbour is 1.0 -> 0x3F80.
+    # mode 1: rne_bf16(cs): 1 + 2^-8 + 2^-10 is above the tie -> 1 + 2^-7; rne_bf16(rs): 1 - 2^-11 is
+    #   2^-11 from 1.0 and 2^-8 - 2^-11 from 1 - 2^-8 -> 1.0; product 1 + 2^-7 -> 0x3F81.
+    ("f16x_double_rounding_bf16_buffers", "bf16", "f16", BF16["1+2^-7"], BF16["1+2^-3"], 0x3C88, 0x3C89),
+    # cs*rs = (1 + 2^-7)(1 + 2^-3) = 1 + 2^-3 + 2^-7 + 2^-10.
+    # mode 0: bf16 ulp 2^-7 in [1, 2): 2^-10 < half ulp -> 1 + 2^-3 + 2^-7, exact in fp16: fraction
+    #   (2^-3 + 2^-7) * 1024 = 128 + 8 = 0x088 -> 0x3C88.
+    # mode 1: both operands exact in fp16, product exact in fp16: fraction 128 + 8 + 1 = 0x089 -> 0x3C89.
+    ("f16_tie_to_even", "f16", "f16", F16["-1.5"] & 0x7FFF, F16["1+2^-10"], 0x3E02, 0x3E02),
+    # 1.5 * (1 + 2^-10) = 1.5 + 2^-10 + 2^-11: fp16 ulp 2^-10 at 1.5, remainder 2^-11 is a tie
+    #   between fraction 0x201 (odd) and 0x202 (even) -> 0x3E02; both modes round the same product once.
+    ("f16_negative_tie", "f16", "f16", F16["-1.5"], F16["1+2^-10"], 0xBE02, 0xBE02),
+    # the same with the sign bit set.
+    ("bf16x_fp16_product_overflow", "f16", "bf16", 0x7B53, 0x4000, 0x7F80, 0x47EA),
+    # cs = 60000 (fp16 0x7B53: 2^15 * (1 + 851/1024)), rs = 2.
+    # mode 0: the fp16 product 120000 exceeds 65504 -> +inf (0x7C00) -> bf16 +inf 0x7F80.
+    # mode 1: rne_bf16(60000): 60000 / 2^15 = 1.8310546875 and 0.8310546875 * 128 = 106.375 -> fraction 106,
+    #   1 + 106/128 = 1.828125, * 2^15 = 59904; * 2 = 119808 = 2^16 * 1.828125 -> exponent field
+    #   127 + 16 = 143 = 0x8F, fraction 106 = 0x6A -> (0x8F << 7) | 0x6A = 0x47EA.
+    ("bf16x_subnormal_tie", "f16", "bf16", 0x0003, F16["0.5"], 0x3400, 0x33C0),
+    # cs = 3 * 2^-24 (fp16 subnormal 3), rs = 0.5: product 1.5 * 2^-24.
+    # mode 0: fp16 subnormal unit 2^-24: 1.5 is a tie between 1 (odd) and 2 (even) -> 2 * 2^-24 = 2^-23,
+    #   bf16 exponent field 127 - 23 = 104 = 0x68 -> 0x3400.
+    # mode 1: 3 * 2^-24 and 0.5 are exact in bf16 and so is their product 1.5 * 2^-24: exponent field
+    #   127 - 24 = 103 = 0x67, fraction 0.5 * 128 = 0x40 -> (0x67 << 7) | 0x40 = 0x33C0.
+]
+
 ACTIVE = [
     {"stages_per_split": [3], "effective": 3, "expected": [0, 1, 2]},
     {"stages_per_split": [3], "effective": 1, "expected": [0]},
@@ -122,6 +167,9 @@ def main() -> None:
             "expected_bits": c["expected"],
         })
     (HERE / "reconstruct_golden.json").write_text(json.dumps(out, indent=1) + "\n")
+    route = [{"name": n, "buffer_dtype": b, "x_dtype": x, "codebook_sum_bits": c, "row_scale_bits": r,
+              "mode0_bits": e0, "mode1_bits": e1} for n, b, x, c, r, e0, e1 in ROUTE]
+    (HERE / "route_golden.json").write_text(json.dumps(route, indent=1) + "\n")
     (HERE / "active_stages.json").write_text(json.dumps(ACTIVE, indent=1) + "\n")
 
 

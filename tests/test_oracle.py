@@ -211,6 +211,56 @@ def test_triton_semantics_closed_form():
     assert torch.allclose(out.double(), want, rtol=1e-6, atol=1e-7)
 
 
+def test_triton_semantics_row_scale_on_accumulator():
+    """The Triton kernel applies the row scale to the fp32 accumulator, not
+    to each weight (src/triton_id_matmul.py:212-216).  Pinned three ways:
+    * power-of-two scales: out = rho * x @ round_x(sum_s cb)^T, the product
+      exact in fp32, against the float64 closed form;
+    * scales in [0.5, 1.5): the same closed form in float64, within fp32
+      rounding (rtol 2e-6);
+    * a planted mistake, the scale folded into each rounded weight
+      (round_x(round_x(w) * rho)), misses that bound by orders of magnitude,
+      so the check tells the two apart."""
+    g = torch.Generator().manual_seed(19)
+    S, N, B, d, K = 2, 24, 6, 8, 64
+    ids = torch.randint(0, K, (S, N, B), generator=g).to(torch.uint8)
+    cb = (torch.randn(S, K, d, generator=g) * 0.05).to(torch.float16)
+    x = torch.randn(4, B * d, generator=g).to(torch.bfloat16)
+    w = ref_ops.triton_rvq_matmul_weight(ids, cb, torch.bfloat16).double()  # [N, B*d] in x dtype
+    base = x.double() @ w.t()
+    pow2 = torch.tensor([2.0 ** ((i % 7) - 3) for i in range(N)], dtype=torch.float16)
+    out = c_oracle.triton_rvq_matmul(x, ids, cb, pow2, out_dtype=torch.float32).double()
+    assert torch.allclose(out, base * pow2.double(), rtol=1e-6, atol=0)
+    rho = (torch.rand(N, generator=g) + 0.5).to(torch.float16)
+    out = c_oracle.triton_rvq_matmul(x, ids, cb, rho, out_dtype=torch.float32).double()
+    want = base * rho.double()
+    assert float(((out - want).abs() / want.abs().max()).max()) <= 2e-6
+    planted = x.double() @ (w * rho.double().unsqueeze(1)).to(torch.bfloat16).double().t()
+    assert float(((planted - want).abs() / want.abs().max()).max()) > 1e-4
+    # a dropped scale is caught too
+    assert not torch.allclose(c_oracle.triton_rvq_matmul(x, ids, cb, torch.ones(N, dtype=torch.float16),
+                                                         out_dtype=torch.float32).double(), want, rtol=1e-3)
+
+
+def test_id_route_weight_golden():
+    """Hand-derived fp16/bf16 rounding of both route modes (mode 0: product in
+    the buffers' dtype then cast, src/runtime.py:89-97; mode 1: operands cast
+    to x dtype then multiplied, src/triton_id_matmul.py:59-60), including
+    double-rounding ties, an fp16 overflow only mode 0 takes and a subnormal
+    tie (tests/golden/route_golden.json, derivations in make_golden.py)."""
+    cases = json.loads((GOLDEN / "route_golden.json").read_text())
+    dt = {"f16": torch.float16, "bf16": torch.bfloat16}
+    for c in cases:
+        bdt, xdt = dt[c["buffer_dtype"]], dt[c["x_dtype"]]
+        sgn = lambda v: v - 0x10000 if v >= 0x8000 else v
+        cs = torch.tensor([sgn(c["codebook_sum_bits"])], dtype=torch.int16).view(bdt)
+        rs = torch.tensor([[sgn(c["row_scale_bits"])]], dtype=torch.int16).view(bdt)
+        ids = torch.zeros(1, 1, dtype=torch.int16)
+        for mode in (0, 1):
+            got = c_oracle.id_route_weight(ids, cs, rs, mode=mode, x_dtype=xdt)
+            assert int(bits(got).reshape(-1)[0]) & 0xFFFF == c[f"mode{mode}_bits"], (c["name"], mode)
+
+
 def test_id_route_weight_matches_torch_ops():
     g = torch.Generator().manual_seed(10)
     ids = torch.randint(0, 300, (9, 40), generator=g).to(torch.int16)

@@ -214,5 +214,22 @@ def require_rocm(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
+def id_range(*ids: torch.Tensor) -> tuple[int, int]:
+    """(min, max) over index tensors of any id dtype, with one host sync.
+    uint16 planes are widened through an int16 view (torch has no uint16
+    reductions on ROCm devices)."""
+    lo, hi = [], []
+    for t in ids:
+        if t.numel() == 0:
+            continue
+        w = (t.view(torch.int16).to(torch.int32) & 0xFFFF) if t.dtype == torch.uint16 else t
+        lo.append(w.amin().to(torch.int64))
+        hi.append(w.amax().to(torch.int64))
+    if not lo:
+        return 0, -1
+    a, b = torch.stack([torch.stack(lo).min(), torch.stack(hi).max()]).tolist()
+    return int(a), int(b)
+
+
 def stream_ptr(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream

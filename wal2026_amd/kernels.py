@@ -48,7 +48,7 @@ def rvq_group_linear_matmul(
     if rho.numel() != n:
         raise ValueError(f"Row-scale mismatch: {n} != {rho.numel()}")
     if ids.numel():
-        lo, hi = torch.stack([ids.amin().to(torch.int64), ids.amax().to(torch.int64)]).tolist()
+        lo, hi = _lib.id_range(ids)
         if lo < 0 or hi >= cbs.shape[1]:
             raise IndexError(f"stage_ids hold index range [{lo}, {hi}] outside [0, {cbs.shape[1]})")
     out = torch.empty(m, n, dtype=x.dtype, device=dev)
@@ -89,7 +89,7 @@ def id_route_linear_matmul(
         raise ValueError(f"row_scale dtype {rho.dtype} must match codebook_sum dtype {lut.dtype}")
     n, k = ids2.shape
     if ids2.numel():
-        lo, hi = torch.stack([ids2.amin().to(torch.int64), ids2.amax().to(torch.int64)]).tolist()
+        lo, hi = _lib.id_range(ids2)
         if lo < 0 or hi >= lut.numel():
             raise IndexError(f"ids hold index range [{lo}, {hi}] outside [0, {lut.numel()})")
     out = torch.empty(x2.shape[0], n, dtype=x.dtype, device=dev)

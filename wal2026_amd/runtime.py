@@ -93,7 +93,7 @@ class _LayerDesc:
                 raise NotImplementedError("wal2026_amd: row groups of one layer must share stage count, block size, "
                                           "codebook size and dtypes")
         arr = (_lib.WalGroup * len(groups))()
-        id_lo, id_hi = [], []
+        all_ids = []
         for i, ((r0, r1), g) in enumerate(zip(row_slices, groups)):
             w = arr[i]
             for s in range(S):
@@ -106,9 +106,7 @@ class _LayerDesc:
                     raise ValueError(f"group {i} stage {s}: unexpected buffer shape")
                 w.stage_ids[s] = ids.data_ptr()
                 w.codebooks[s] = cb.data_ptr()
-                wide = ids.view(torch.int16).to(torch.int32) & 0xFFFF if ids.dtype == torch.uint16 else ids
-                id_lo.append(wide.amin().to(torch.int64))
-                id_hi.append(wide.amax().to(torch.int64))
+                all_ids.append(ids)
             rs = g.row_scale.reshape(-1)
             if rs.numel() != r1 - r0:
                 raise ValueError(f"group {i}: row_scale has {rs.numel()} entries for {r1 - r0} rows")
@@ -125,7 +123,7 @@ class _LayerDesc:
         # ids must index the codebook: the reference's gather raises on a bad
         # index; here a bad index is refused before any launch (one host sync
         # when the descriptor is built, never per forward).
-        lo, hi = torch.stack([torch.stack(id_lo).min(), torch.stack(id_hi).max()]).tolist()
+        lo, hi = _lib.id_range(*all_ids)
         if lo < 0 or hi >= K:
             raise IndexError(f"stage_ids hold index range [{lo}, {hi}] outside [0, codebook_size={K})")
         scale_dt = g0.row_scale.dtype
