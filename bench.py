@@ -220,6 +220,137 @@ def bench_encoder(args) -> int:
     return 0
 
 
+class Stack:
+    """A seeded stack of compressed linears of one config on the GPU, with the
+    drop-in (one launch per linear) and fused (linears sharing an input in one
+    launch) steps."""
+
+    def __init__(self, cfg: synth.Config, layers: int, dev: torch.device):
+        self.cfg, self.layers, self.dev = cfg, layers, dev
+        self.stack = build_stack(cfg, dev, layers)
+        gen = synth.generator(1, dev)
+        self.xs = {k: synth.make_activation(cfg.m, k, cfg.x_dtype, gen, dev) for k in {k for _, _, k in cfg.shapes()}}
+        names = [n for n, _, _ in cfg.shapes()]
+        self.fuse = [(f, members) for f, members in FUSION_GROUPS if all(m in names for m in members)]
+        for layer in self.stack:
+            for f, members in self.fuse:
+                layer[f] = FusedBlockRVQLinears([layer[m] for m in members])
+        self.shape = {n: (o, k) for n, o, k in cfg.shapes()}
+
+    def fused_launches(self):
+        """(name, in_features, compressed bytes) of the fused step's launches."""
+        cfg, shape = self.cfg, self.shape
+        fused_members = {m for _, members in self.fuse for m in members}
+        out = [(f, shape[members[0]][1], sum(linear_bytes(cfg, *shape[m]) for m in members)) for f, members in self.fuse]
+        out += [(n, k, linear_bytes(cfg, o, k)) for n, o, k in cfg.shapes() if n not in fused_members]
+        return out
+
+    def dominant(self):
+        return max(self.fused_launches(), key=lambda t: t[2])
+
+    def launch_flops(self, name: str) -> int:
+        members = dict(self.fuse).get(name, (name,))
+        return sum(2 * self.cfg.m * self.shape[m][0] * self.shape[m][1] for m in members)
+
+    def step_unfused(self):
+        """The drop-in step: every linear its own forward (the reference's call pattern)."""
+        for layer in self.stack:
+            for name, _n, k in self.cfg.shapes():
+                layer[name](self.xs[k])
+
+    def step_fused(self):
+        for layer in self.stack:
+            for name, k, _b in self.fused_launches():
+                layer[name](self.xs[k])
+
+    def graph_ms(self, step, steps: int, warmup: int) -> float:
+        """ms per replay of one step captured as a HIP graph (steps replays timed)."""
+        step()  # builds descriptors and codebook images outside the graph
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1000.0 / steps
+
+    def eager_ms(self, step, steps: int, warmup: int) -> tuple[float, float]:
+        """(ms per step, host ms per step) of plain eager forwards (no graph):
+        what an import swap gives when the host issues every launch; the host
+        figure is the time to issue the steps, before waiting for the GPU."""
+        for _ in range(max(warmup, 1)):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        t_issue = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1000.0 / steps, t_issue * 1000.0 / steps
+
+    def launch_us(self, name: str, reps: int = 3) -> float:
+        k = next(kk for n, kk, _ in self.fused_launches() if n == name) if name in dict(self.fuse) \
+            else self.shape[name][1]
+        return time_kernel_family([layer[name] for layer in self.stack], self.xs[k], reps=reps)
+
+
+def roofline_of(st: Stack, name: str, nbytes: int, us: float, pmc_summary: str | None) -> dict:
+    cfg = st.cfg
+    if cfg.m > 16:
+        flops = st.launch_flops(name)
+        tflops = flops / (us * 1e-6) / 1e12
+        return {"bound": "mfma", "kernel": f"rvq_prefill_*_kernel, launcher's choice ({name}, {flops} flop)",
+                "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "avg_launch_us": round(us, 3),
+                "algorithmic_flops_per_launch": flops,
+                "traffic": traffic_bytes(pmc_summary) if pmc_summary else None}
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "kernel": f"rvq_decode_kernel ({name}, {nbytes} compressed bytes)",
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": nbytes,
+            "traffic": traffic_bytes(pmc_summary) if pmc_summary else None}
+
+
+def secondary(name: str, layers: int | None, steps: int, warmup: int, dev: torch.device) -> dict:
+    """One line for another config: fused-step tokens/s over a graph-captured
+    stack and the dominant launch against its roofline (HIP events)."""
+    cfg = synth.CONFIGS[name]
+    layers = layers or cfg.layers
+    log(f"secondary {name}: building {layers} layers")
+    st = Stack(cfg, layers, dev)
+    ms = st.graph_ms(st.step_fused, steps, warmup)
+    dom_name, _k, dom_bytes = st.dominant()
+    us = st.launch_us(dom_name)
+    kind = "prefill" if cfg.m > 16 else "decode"
+    us_layer = ms * 1000.0 / layers
+    out = {"workload": f"{name}: {kind} M={cfg.m}, S={cfg.num_stages}, K={cfg.codebook_size}, "
+                       f"{str(cfg.ids_dtype()).replace('torch.', '')} ids, {layers} of {cfg.layers} layers timed, "
+                       f"fused, one HIP graph per step, {steps} steps; tok/s over all {cfg.layers} layers",
+           "tok_s": round(cfg.m * 1e6 / (us_layer * cfg.layers), 2), "us_per_layer": round(us_layer, 3),
+           "roofline": roofline_of(st, dom_name, dom_bytes, us,
+                                   str(ROOT / "profiles" / f"{kind}_{name}_{dom_name}_pmc.txt"))}
+    if kind == "decode":
+        out["step_hbm_fraction"] = round(cfg.compressed_bytes_per_layer() * layers / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                         4)
+    else:
+        out["tflops_per_step"] = round(cfg.flops_per_layer() * layers / (ms * 1e-3) / 1e12, 1)
+    del st
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -230,6 +361,8 @@ def main() -> int:
     ap.add_argument("--m", type=int, default=None, help="activation rows (default: the config's, 1 for c3)")
     ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the c5 decode and c4 prefill lines the default c3 run adds under config.secondary")
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run the dominant launch N times per layer, then one 256 MiB device copy "
                          "(the calibration kernel); for rocprofv3 --pmc runs")
@@ -258,65 +391,15 @@ def main() -> int:
     layers = args.layers or cfg.layers
     dev = torch.device("cuda", 0)
     log(f"building {layers} layers of {cfg.name} on {torch.cuda.get_device_name(dev)}")
-    stack = build_stack(cfg, dev, layers)
-    gen = synth.generator(1, dev)
-    xs = {k: synth.make_activation(cfg.m, k, cfg.x_dtype, gen, dev) for k in {k for _, _, k in cfg.shapes()}}
-
-    # drop-in step: every linear its own launch (the reference's call pattern)
-    def step_unfused():
-        for layer in stack:
-            for name, _n, k in cfg.shapes():
-                layer[name](xs[k])
-
-    # fused step: linears that read the same activation share one launch
-    names = [n for n, _, _ in cfg.shapes()]
-    fuse = [(f, members) for f, members in FUSION_GROUPS if all(m in names for m in members)]
-    fused_members = {m for _, members in fuse for m in members}
-    for layer in stack:
-        for f, members in fuse:
-            layer[f] = FusedBlockRVQLinears([layer[m] for m in members])
-    shape = {n: (o, k) for n, o, k in cfg.shapes()}
-
-    def fused_launches():
-        """(name, in_features, compressed bytes) of the fused step's launches."""
-        out = [(f, shape[members[0]][1], sum(linear_bytes(cfg, *shape[m]) for m in members)) for f, members in fuse]
-        out += [(n, k, linear_bytes(cfg, o, k)) for n, o, k in cfg.shapes() if n not in fused_members]
-        return out
-
-    def step_fused():
-        for layer in stack:
-            for name, k, _b in fused_launches():
-                layer[name](xs[k])
-
-    def graph_ms(step) -> float:
-        step()  # builds descriptors and codebook images outside the graph
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            step()
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph):
-            step()
-        torch.cuda.synchronize()
-        for _ in range(args.warmup):
-            graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            graph.replay()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) * 1000.0 / args.steps
+    st = Stack(cfg, layers, dev)
 
     if args.profile_dominant:
-        step_fused()  # descriptors and codebook images
+        st.step_fused()  # descriptors and codebook images
         torch.cuda.synchronize()
-        dom_name, dom_k, dom_bytes = max(fused_launches(), key=lambda t: t[2])
+        dom_name, dom_k, dom_bytes = st.dominant()
         for _ in range(args.profile_dominant):
-            for layer in stack:
-                layer[dom_name](xs[dom_k])
+            for layer in st.stack:
+                layer[dom_name](st.xs[dom_k])
         torch.cuda.synchronize()
         src = torch.empty(64 * 2**20, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
@@ -327,56 +410,31 @@ def main() -> int:
         return 0
 
     log(f"timing {args.steps} graph replays of the drop-in step (one launch per linear)")
-    ms_unfused = graph_ms(step_unfused)
-    log(f"timing {args.steps} graph replays of the fused step ({len(fused_launches())} launches per layer)")
-    ms_per_step = graph_ms(step_fused)
+    ms_unfused = st.graph_ms(st.step_unfused, args.steps, args.warmup)
+    log(f"timing {args.steps} eager drop-in steps (no graph)")
+    ms_eager, ms_eager_host = st.eager_ms(st.step_unfused, args.steps, args.warmup)
+    log(f"timing {args.steps} graph replays of the fused step ({len(st.fused_launches())} launches per layer)")
+    ms_per_step = st.graph_ms(st.step_fused, args.steps, args.warmup)
     tok_s = cfg.m * 1000.0 / ms_per_step
-    us_per_layer = ms_per_step * 1000.0 / layers
 
     # dominant kernel: the fused step's largest launch, timed per launch
-    dom_name, dom_k, dom_bytes = max(fused_launches(), key=lambda t: t[2])
+    dom_name, dom_k, dom_bytes = st.dominant()
     log(f"timing the dominant kernel ({dom_name}) per launch")
-    dom_us = time_kernel_family([layer[dom_name] for layer in stack], xs[dom_k])
-    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    dom_us = st.launch_us(dom_name)
     per_launch = {}
-    for name, k, nbytes in fused_launches():
-        us = time_kernel_family([layer[name] for layer in stack], xs[k], reps=1)
+    for name, k, nbytes in st.fused_launches():
+        us = st.launch_us(name, reps=1)
         per_launch[name] = {"us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
     per_linear = {}
     for name, n, k in cfg.shapes():
-        us = time_kernel_family([layer[name] for layer in stack], xs[k], reps=1)
+        us = st.launch_us(name, reps=1)
         per_linear[name] = {"us": round(us, 3), "GBps": round(linear_bytes(cfg, n, k) / (us * 1e-6) / 1e9, 1)}
     layer_bytes = cfg.compressed_bytes_per_layer()
     prefill = cfg.m > 16
     kind = "prefill" if prefill else "decode"
     pmc_summary = args.pmc_summary or str(ROOT / "profiles" / f"{kind}_{cfg.name}_{dom_name}_pmc.txt")
-    if prefill:
-        dom_flops = sum(2 * cfg.m * shape[m_][0] * shape[m_][1] for f, members in fuse if f == dom_name
-                        for m_ in members) or 2 * cfg.m * shape[dom_name][0] * shape[dom_name][1]
-        tflops = dom_flops / (dom_us * 1e-6) / 1e12
-        roofline = {
-            "bound": "mfma",
-            "kernel": f"rvq_prefill_tall/wide_kernel, launcher's choice ({dom_name}, {dom_flops} flop)",
-            "achieved": round(tflops, 1),
-            "peak": BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-            "avg_launch_us": round(dom_us, 3),
-            "algorithmic_flops_per_launch": dom_flops,
-            "traffic": traffic_bytes(pmc_summary),
-        }
-    else:
-        roofline = {
-            "bound": "hbm",
-            "kernel": f"rvq_decode_kernel ({dom_name}, {dom_bytes} compressed bytes)",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "avg_launch_us": round(dom_us, 3),
-            "algorithmic_bytes_per_launch": dom_bytes,
-            "traffic": traffic_bytes(pmc_summary),
-        }
+    roofline = roofline_of(st, dom_name, dom_bytes, dom_us, pmc_summary)
+    n_linears = len(cfg.shapes()) * layers
 
     result = {
         "metric": "RVQ-GEMV us/layer & %HBM roofline (M=1); decode tok/s at Llama-8B shapes",
@@ -396,14 +454,17 @@ def main() -> int:
                         f"S={cfg.num_stages}, K={cfg.codebook_size}, d={cfg.block_size}, "
                         f"{str(cfg.ids_dtype()).replace('torch.', '')} ids, scale per {cfg.scale_rows} rows, "
                         f"{kind} M={cfg.m}, one HIP graph per step; linears sharing an input fused "
-                        f"({', '.join(f for f, _ in fuse)})",
+                        f"({', '.join(f for f, _ in st.fuse)})",
             "layers": layers,
             "m": cfg.m,
-            "us_per_layer": round(us_per_layer, 3),
+            "us_per_layer": round(ms_per_step * 1000.0 / layers, 3),
             "compressed_bytes_per_layer": layer_bytes,
             "step_hbm_fraction": round(layer_bytes * layers / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "unfused_tok_s": round(cfg.m * 1000.0 / ms_unfused, 3),
             "unfused_us_per_layer": round(ms_unfused * 1000.0 / layers, 3),
+            "eager_unfused_tok_s": round(cfg.m * 1000.0 / ms_eager, 3),
+            "eager_us_per_forward": round(ms_eager * 1000.0 / n_linears, 3),
+            "eager_host_issue_us_per_forward": round(ms_eager_host * 1000.0 / n_linears, 3),
             "per_launch": per_launch,
             "per_linear_unfused": per_linear,
         },
@@ -411,6 +472,13 @@ def main() -> int:
     }
     if prefill:
         result["config"]["tflops_per_step"] = round(cfg.flops_per_layer() * layers / (ms_per_step * 1e-3) / 1e12, 1)
+    del st
+    torch.cuda.empty_cache()
+    if not args.no_secondary and args.config == "c3" and args.m is None and args.layers is None:
+        result["config"]["secondary"] = {
+            "c5": secondary("c5", None, 128, args.warmup, dev),
+            "c4": secondary("c4", 4, 10, 2, dev),
+        }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(cfg)

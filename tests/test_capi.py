@@ -282,3 +282,14 @@ def test_decode_falls_back_when_no_layout_fits(monkeypatch):
     L, _g = _bench_layer([64], 128, 1, 9712, _lib.U16)
     assert _info(L, 1)[1].kernel == _lib.KERNEL_DECODE
     assert _info(L, 16)[1].kernel == _lib.KERNEL_GENERIC
+
+
+def test_torch_operator_library_loads_and_refuses_cpu():
+    """libwal2026_amd_torch.so registers torch.ops.wal2026_amd.rvq_linear over
+    the C ABI; a CPU tensor is refused with RuntimeError (there is no CPU
+    path), before the layer descriptor is touched."""
+    import torch
+
+    op = _lib.ops().rvq_linear
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        op(torch.zeros(1, 64, dtype=torch.bfloat16), 0, 0, 0, None, None)

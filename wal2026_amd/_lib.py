@@ -12,6 +12,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libwal2026_amd.so"
+TORCH_OPS_PATH = Path(__file__).resolve().parent / "_lib" / "libwal2026_amd_torch.so"
 
 MAX_STAGES = 8
 ABI_VERSION = 3
@@ -171,6 +172,24 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(f"wal2026_amd: ABI {L.wal_abi_version()} != {ABI_VERSION}")
         _lib = L
     return _lib
+
+
+_ops = None
+
+
+def ops():
+    """torch.ops.wal2026_amd: the PyTorch-ROCm operators over the C ABI
+    (libwal2026_amd_torch.so, built beside the library; raises if missing)."""
+    global _ops
+    if _ops is None:
+        lib()  # the operator library links it: load (and version-check) it first
+        path = Path(os.environ.get("WAL2026_AMD_TORCH_LIB", TORCH_OPS_PATH))
+        if not path.exists():
+            raise RuntimeError(f"wal2026_amd: {path} is missing; build it with `python -m wal2026_amd.build` "
+                               "(the HIP library is required, there is no fallback path)")
+        torch.ops.load_library(str(path))
+        _ops = torch.ops.wal2026_amd
+    return _ops
 
 
 def check(status: int) -> None:

@@ -44,6 +44,8 @@ COMMON_FLAGS = [
 ]
 
 SOURCES = sorted(CSRC.glob("*.hip"))
+TORCH_OPS_SRC = CSRC / "torch_ops.cpp"
+TORCH_OPS_LIB = LIBDIR / "libwal2026_amd_torch.so"
 HEADERS = sorted(CSRC.glob("*.h")) + sorted(INCLUDE.glob("*.h"))
 
 
@@ -73,8 +75,35 @@ def device_asm(src: Path, out: Path) -> Path:
     return out
 
 
+def _torch_ops_cmd(out: Path) -> list[str]:
+    """g++ line of the PyTorch-ROCm operator library (host code only: it
+    calls the C ABI, links libwal2026_amd.so beside it)."""
+    import torch
+    from torch.utils import cpp_extension as ce
+
+    abi = int(torch.compiled_with_cxx11_abi())
+    cmd = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-I{INCLUDE}"]
+    cmd += [f"-I{p}" for p in ce.include_paths(device_type="cuda")]
+    cmd += [str(TORCH_OPS_SRC), "-o", str(out), f"-L{LIBDIR}", "-lwal2026_amd", "-Wl,-rpath,$ORIGIN"]
+    for p in ce.library_paths(device_type="cuda"):
+        cmd += [f"-L{p}", f"-Wl,-rpath,{p}"]
+    cmd += ["-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch", "-lamdhip64"]
+    return cmd
+
+
+def build_torch_ops() -> Path:
+    """Build libwal2026_amd_torch.so (needs libwal2026_amd.so)."""
+    tmp = TORCH_OPS_LIB.with_suffix(".so.tmp")
+    r = subprocess.run(_torch_ops_cmd(tmp), capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"torch op library failed to build:\n{r.stderr}")
+    os.replace(tmp, TORCH_OPS_LIB)
+    return TORCH_OPS_LIB
+
+
 def build(jobs: int | None = None) -> Path:
-    """Compile and link the library; always rebuilds."""
+    """Compile and link the library and its torch operator; always rebuilds."""
     BUILD.mkdir(parents=True, exist_ok=True)
     LIBDIR.mkdir(parents=True, exist_ok=True)
     jobs = jobs or min(len(SOURCES), max(1, (os.cpu_count() or 4)))
@@ -86,6 +115,7 @@ def build(jobs: int | None = None) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_torch_ops()
     return LIB
 
 

@@ -1,0 +1,84 @@
+// torch_ops.cpp -- the PyTorch-ROCm operator over the C ABI (libwal2026_amd_torch.so).
+//
+// One op per hot call, registered as torch.ops.wal2026_amd.*: the module
+// forward of the reference's PackedGroupedBlockRVQLinear
+// (src/runtime.py:1362-1507) reaches the kernels through it instead of
+// ctypes.  The op checks its tensors with TORCH_CHECK (a failed check, or an
+// error status of the library, raises RuntimeError -- the exception the
+// reference's fused-kernel callers catch, src/runtime.py:1655-1661),
+// allocates the output with torch's caching allocator and launches on the
+// current HIP stream, so it is safe under HIP graph capture.  The layer
+// descriptor (struct wal_rvq_layer with its plan and codebook image) is built
+// once by the Python layer and passed as its address; it must outlive the
+// call.
+#include <ATen/ATen.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "wal2026_amd.h"
+
+namespace {
+
+int dtype_tag(at::ScalarType t) {
+  switch (t) {
+    case at::kHalf: return WAL_F16;
+    case at::kBFloat16: return WAL_BF16;
+    case at::kFloat: return WAL_F32;
+    default: return -1;
+  }
+}
+
+// y[..., out_features] = x[..., in_features] W^T (+ bias) for the layer at
+// address `layer` (a wal_rvq_layer*): wal_rvq_linear on the current stream.
+at::Tensor rvq_linear(const at::Tensor& x, int64_t layer, int64_t semantics, int64_t stage_mask,
+                      const c10::optional<at::Tensor>& bias, c10::optional<at::ScalarType> out_dtype) {
+  const wal_rvq_layer* L = reinterpret_cast<const wal_rvq_layer*>(layer);
+  TORCH_CHECK(L != nullptr, "wal2026_amd: null layer descriptor");
+  TORCH_CHECK(x.is_cuda(), "wal2026_amd: x must be on a ROCm device (got ", x.device(), ")");
+  TORCH_CHECK(x.dim() >= 1 && x.size(-1) == L->in_features, "wal2026_amd: x has ", x.size(-1),
+              " features, the layer ", L->in_features);
+  const int xt = dtype_tag(x.scalar_type());
+  TORCH_CHECK(xt >= 0, "wal2026_amd: unsupported activation dtype ", x.scalar_type());
+  at::Tensor xc = x.contiguous();
+  if (reinterpret_cast<uintptr_t>(xc.data_ptr()) % 16 != 0) xc = xc.clone();  // the fused kernels load 16 B
+  const at::ScalarType yt = out_dtype.has_value() ? *out_dtype : x.scalar_type();
+  TORCH_CHECK(dtype_tag(yt) >= 0, "wal2026_amd: unsupported output dtype ", yt);
+  std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end());
+  shape.back() = L->out_features;
+  at::Tensor y = at::empty(shape, x.options().dtype(yt));
+  const int64_t m = x.numel() / L->in_features;
+  if (m == 0) return y;
+  const void* b = nullptr;
+  int bt = WAL_F32;
+  at::Tensor bc;
+  if (bias.has_value() && bias->defined()) {
+    bc = bias->contiguous();
+    TORCH_CHECK(bc.is_cuda() && bc.device() == x.device(), "wal2026_amd: bias must be on the device of x");
+    TORCH_CHECK(bc.numel() == L->out_features, "wal2026_amd: bias has ", bc.numel(), " entries for ",
+                L->out_features, " outputs");
+    bt = dtype_tag(bc.scalar_type());
+    TORCH_CHECK(bt >= 0, "wal2026_amd: unsupported bias dtype ", bc.scalar_type());
+    b = bc.data_ptr();
+  }
+  hipStream_t st = c10::hip::getCurrentHIPStream(x.device().index()).stream();
+  const int rc = wal_rvq_linear(L, (int)semantics, (uint32_t)stage_mask, xc.data_ptr(), m, xt, b, bt, y.data_ptr(),
+                                dtype_tag(yt), st);
+  TORCH_CHECK(rc == WAL_OK, "wal2026_amd error ", rc, ": ", wal_last_error());
+  return y;
+}
+
+// Tensors on the CPU are refused loudly: the library is the only compute path.
+at::Tensor rvq_linear_cpu(const at::Tensor& x, int64_t, int64_t, int64_t, const c10::optional<at::Tensor>&,
+                          c10::optional<at::ScalarType>) {
+  TORCH_CHECK(false, "wal2026_amd: x must be on a ROCm device (got ", x.device(),
+              "); the HIP library is the only compute path");
+}
+
+}  // namespace
+
+TORCH_LIBRARY(wal2026_amd, m) {
+  m.def("rvq_linear(Tensor x, int layer, int semantics, int stage_mask, Tensor? bias, ScalarType? out_dtype) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(wal2026_amd, CUDA, m) { m.impl("rvq_linear", rvq_linear); }
+TORCH_LIBRARY_IMPL(wal2026_amd, CPU, m) { m.impl("rvq_linear", rvq_linear_cpu); }

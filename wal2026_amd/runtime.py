@@ -191,6 +191,10 @@ class _LayerDesc:
         return call
 
 
+# Bumped whenever a group's active stages change, so that layers holding a
+# cached call (with its stage mask) rebuild it.
+_STAGE_EPOCH = [0]
+
 _SCALE_RUNS = (128, 64, 32, 16)
 
 
@@ -332,6 +336,7 @@ class PackedBlockRVQGroup(nn.Module):
     def set_effective_stages_per_split(self, k: int) -> None:
         self.effective_stages_per_split = int(k)
         self._active_stage_indices = None
+        _STAGE_EPOCH[0] += 1
 
     def active_stage_mask(self) -> int:
         mask = 0
@@ -479,6 +484,8 @@ class PackedGroupedBlockRVQLinear(nn.Module):
         else:
             self.bias = None
         self._desc: _LayerDesc | None = None
+        # (device, x dtype, fast) -> (layer address, semantics, stage mask, stage epoch, layer struct)
+        self._calls: dict = {}
         prev = 0
         for r0, r1 in self.row_slices:
             if r0 != prev or r1 <= r0:
@@ -489,19 +496,40 @@ class PackedGroupedBlockRVQLinear(nn.Module):
 
     def _apply(self, fn, recurse: bool = True):
         self._desc = None
+        self._calls = {}
         return super()._apply(fn, recurse)
 
     def invalidate_caches(self) -> None:
-        """Drop the cached descriptors and codebook images of the layer and
-        its groups (rebuilt on the next call); needed after changing buffers in
-        place."""
+        """Drop the cached descriptors, calls and codebook images of the layer
+        and its groups (rebuilt on the next call); needed after changing or
+        replacing buffers other than through .to() / load_state_dict."""
         self._desc = None
+        self._calls = {}
         for g in self.groups:
             g.invalidate_caches()
 
     def _load_from_state_dict(self, *args, **kwargs):
         self._desc = None  # the groups reset their own caches
+        self._calls = {}
         return super()._load_from_state_dict(*args, **kwargs)
+
+    def _call_for(self, x: Tensor, fast: bool):
+        """The cached (layer address, semantics, stage mask) of a call on x's
+        device and dtype, built on first use; None when the groups decode
+        different stage subsets (one launch per group then)."""
+        key = (x.device, x.dtype, fast)
+        c = self._calls.get(key)
+        if c is not None and c[3] == _STAGE_EPOCH[0]:
+            return c
+        _lib.require_rocm(x, self.groups[0].row_scale)
+        sem = _lib.RECONSTRUCT_FAST if fast else _lib.RECONSTRUCT
+        mask = self._uniform_mask() if fast else 0
+        if mask is None:
+            return None
+        layer = self._descriptor().layer_for(sem, x.dtype)
+        c = (ctypes.addressof(layer), sem, mask, _STAGE_EPOCH[0], layer)
+        self._calls[key] = c
+        return c
 
     def _descriptor(self) -> _LayerDesc:
         dev = self.groups[0].row_scale.device
@@ -546,38 +574,26 @@ class PackedGroupedBlockRVQLinear(nn.Module):
         return _launch_info(self._descriptor().layer, _lib.RECONSTRUCT_FAST if fast else _lib.RECONSTRUCT, x)
 
     # -- forward -------------------------------------------------------------
-    def _hip_linear(self, x_flat: Tensor, fast: bool, out_dtype: torch.dtype | None = None) -> Tensor:
-        dev = _lib.require_rocm(x_flat, self.groups[0].row_scale)
-        x_c = x_flat.contiguous()
-        if x_c.data_ptr() % 16:
-            x_c = x_c.clone()
-        M = x_c.shape[0]
-        y = torch.empty(M, self.out_features, dtype=out_dtype or x_flat.dtype, device=dev)
-        if M == 0:
-            return y
-        lib = _lib.lib()
-        bias = self.bias
-        btag = _lib.float_tag(bias.dtype) if bias is not None else _lib.F32
-        sem = _lib.RECONSTRUCT_FAST if fast else _lib.RECONSTRUCT
-        mask = self._uniform_mask() if fast else 0
-        stream = _lib.stream_ptr(dev)
-        if mask is None:
-            # groups decode different stage subsets: one launch per group
-            for (r0, r1), g in zip(self.row_slices, self.groups):
-                part = torch.empty(M, r1 - r0, dtype=y.dtype, device=dev)
-                d = g._descriptor()
-                b = None if bias is None else bias[r0:r1].contiguous()
-                _lib.check(lib.wal_rvq_linear(ctypes.byref(d.layer_for(sem, x_c.dtype)), sem, g.active_stage_mask(),
-                                              x_c.data_ptr(), M,
-                                              _lib.float_tag(x_c.dtype), _ptr(b), btag, part.data_ptr(),
-                                              _lib.float_tag(y.dtype), stream))
-                y[:, r0:r1] = part
-            return y
-        desc = self._descriptor()
-        _lib.check(lib.wal_rvq_linear(ctypes.byref(desc.layer_for(sem, x_c.dtype)), sem, mask, x_c.data_ptr(), M,
-                                      _lib.float_tag(x_c.dtype), _ptr(bias), btag, y.data_ptr(),
-                                      _lib.float_tag(y.dtype), stream))
-        return y
+    def _hip_linear(self, x: Tensor, fast: bool, out_dtype: torch.dtype | None = None) -> Tensor:
+        """reconstruct_weight(_fast) arithmetic and the contraction, one
+        launch for every row group, through the torch operator
+        (torch.ops.wal2026_amd.rvq_linear); y has x's leading dims."""
+        c = self._call_for(x, fast)
+        if c is not None:
+            return _lib.ops().rvq_linear(x, c[0], c[1], c[2], self.bias, out_dtype)
+        # groups decode different stage subsets: one launch per group
+        dev = x.device
+        lead = x.shape[:-1]
+        x_flat = x.reshape(-1, x.shape[-1])
+        M = x_flat.shape[0]
+        y = torch.empty(M, self.out_features, dtype=out_dtype or x.dtype, device=dev)
+        sem = _lib.RECONSTRUCT_FAST
+        for (r0, r1), g in zip(self.row_slices, self.groups):
+            layer = g._descriptor().layer_for(sem, x.dtype)
+            b = None if self.bias is None else self.bias[r0:r1]
+            y[:, r0:r1] = _lib.ops().rvq_linear(x_flat, ctypes.addressof(layer), sem, g.active_stage_mask(), b,
+                                                out_dtype)
+        return y.reshape(*lead, self.out_features)
 
     def _stagewise(self, x_flat: Tensor, out_dtype: torch.dtype | None = None) -> Tensor:
         """Strategy stagewise_einsum (src/runtime.py:1466-1475): every group's
@@ -603,14 +619,14 @@ class PackedGroupedBlockRVQLinear(nn.Module):
         return torch.cat(parts, dim=-1)
 
     def forward(self, x: Tensor) -> Tensor:
-        orig = x.shape
-        x_flat = x.reshape(-1, orig[-1])
         s = self.matmul_strategy
         if s in _RECON_STRATEGIES:
-            out = self._hip_linear(x_flat, fast=False)
-        elif s in _FAST_STRATEGIES:
-            out = self._hip_linear(x_flat, fast=True)
-        elif s == "triton_block_rvq":
+            return self._hip_linear(x, fast=False)
+        if s in _FAST_STRATEGIES:
+            return self._hip_linear(x, fast=True)
+        orig = x.shape
+        x_flat = x.reshape(-1, orig[-1])
+        if s == "triton_block_rvq":
             out = self._triton_strategy(x_flat)
         elif s == "stagewise_einsum":
             out = self._stagewise(x_flat)
@@ -658,6 +674,7 @@ class FusedBlockRVQLinears(nn.Module):
         self.out_features = [lin.out_features for lin in linears]
         self._desc: _LayerDesc | None = None
         self._bias: Tensor | None = None
+        self._calls: dict = {}  # (device, x dtype) -> (layer address, semantics, mask, stage epoch, layer)
 
     def _groups_and_slices(self):
         groups, slices, base = [], [], 0
@@ -684,6 +701,26 @@ class FusedBlockRVQLinears(nn.Module):
     def invalidate_caches(self) -> None:
         self._desc = None
         self._bias = None
+        self._calls = {}
+
+    def _call_for(self, x: Tensor):
+        key = (x.device, x.dtype)
+        c = self._calls.get(key)
+        if c is not None and c[3] == _STAGE_EPOCH[0]:
+            return c
+        _lib.require_rocm(x, self._linears[0].groups[0].row_scale)
+        desc = self._descriptor()
+        sem = _lib.RECONSTRUCT_FAST if self._fast else _lib.RECONSTRUCT
+        mask = 0
+        if self._fast:
+            masks = {g.active_stage_mask() for lin in self._linears for g in lin.groups}
+            if len(masks) != 1:
+                raise ValueError("fused reconstruct_weight_fast linears must decode the same stages")
+            mask = masks.pop()
+        layer = desc.layer_for(sem, x.dtype)
+        c = (ctypes.addressof(layer), sem, mask, _STAGE_EPOCH[0], layer)
+        self._calls[key] = c
+        return c
 
     def launch_info(self, x: Tensor) -> dict:
         """Which kernel variant forward(x) launches (see
@@ -691,32 +728,11 @@ class FusedBlockRVQLinears(nn.Module):
         return _launch_info(self._descriptor().layer, _lib.RECONSTRUCT_FAST if self._fast else _lib.RECONSTRUCT, x)
 
     def forward(self, x: Tensor) -> tuple[Tensor, ...]:
-        orig = x.shape
-        x_flat = x.reshape(-1, orig[-1])
-        dev = _lib.require_rocm(x_flat, self._linears[0].groups[0].row_scale)
-        x_c = x_flat.contiguous()
-        if x_c.data_ptr() % 16:
-            x_c = x_c.clone()
-        desc = self._descriptor()
-        total = sum(self.out_features)
-        M = x_c.shape[0]
-        y = torch.empty(M, total, dtype=x_flat.dtype, device=dev)
-        if M:
-            sem = _lib.RECONSTRUCT_FAST if self._fast else _lib.RECONSTRUCT
-            mask = 0
-            if self._fast:
-                masks = {g.active_stage_mask() for lin in self._linears for g in lin.groups}
-                if len(masks) != 1:
-                    raise ValueError("fused reconstruct_weight_fast linears must decode the same stages")
-                mask = masks.pop()
-            bias = self._bias
-            _lib.check(_lib.lib().wal_rvq_linear(
-                ctypes.byref(desc.layer_for(sem, x_c.dtype)), sem, mask, x_c.data_ptr(), M, _lib.float_tag(x_c.dtype),
-                _ptr(bias), _lib.float_tag(bias.dtype) if bias is not None else _lib.F32, y.data_ptr(),
-                _lib.float_tag(y.dtype), _lib.stream_ptr(dev)))
+        c = self._call_for(x)
+        y = _lib.ops().rvq_linear(x, c[0], c[1], c[2], self._bias, None)
         outs, o0 = [], 0
         for n in self.out_features:
-            outs.append(y[:, o0:o0 + n].reshape(*orig[:-1], n))
+            outs.append(y[..., o0:o0 + n])
             o0 += n
         return tuple(outs)
 
