@@ -12,7 +12,7 @@
 #include <set>
 #include <utility>
 
-#include "../../include/wal2026_amd.h"
+#include "wal2026_amd.h"
 #include "rvq_kernels.h"
 
 using namespace wal;
