@@ -35,6 +35,8 @@
 //     compiler's in-order load waits fall back to full drains.)
 #pragma once
 
+#include <type_traits>
+
 #include "rvq_fragment.h"
 
 namespace wal {
@@ -59,6 +61,37 @@ constexpr int decode_prefetch() {
 template <int S, int LMODE>
 constexpr int decode_gather_ahead() {
   return S * lds_entry_bytes<LMODE>() / 4 > 24 ? 1 : 2;
+}
+
+// Each lane gets the value of lane TT of its 16-lane row (DPP row_newbcast).
+template <int TT>
+WAL_DEVICE uint32_t row_bcast_dw(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + TT, 0xf, 0xf, false);
+}
+template <int TT>
+WAL_DEVICE u32x4_t row_bcast_t(const u32x4_t& v) {
+  return u32x4_t{row_bcast_dw<TT>(v[0]), row_bcast_dw<TT>(v[1]), row_bcast_dw<TT>(v[2]), row_bcast_dw<TT>(v[3])};
+}
+// row_bcast_t<tt> for a tt known after unrolling.
+WAL_DEVICE u32x4_t row_bcast(const u32x4_t& v, int tt) {
+  switch (tt) {
+    case 0: return row_bcast_t<0>(v);
+    case 1: return row_bcast_t<1>(v);
+    case 2: return row_bcast_t<2>(v);
+    case 3: return row_bcast_t<3>(v);
+    case 4: return row_bcast_t<4>(v);
+    case 5: return row_bcast_t<5>(v);
+    case 6: return row_bcast_t<6>(v);
+    case 7: return row_bcast_t<7>(v);
+    case 8: return row_bcast_t<8>(v);
+    case 9: return row_bcast_t<9>(v);
+    case 10: return row_bcast_t<10>(v);
+    case 11: return row_bcast_t<11>(v);
+    case 12: return row_bcast_t<12>(v);
+    case 13: return row_bcast_t<13>(v);
+    case 14: return row_bcast_t<14>(v);
+    default: return row_bcast_t<15>(v);
+  }
 }
 
 template <typename IdT>
@@ -430,101 +463,122 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
         // lanes past the row read the 256-byte zero row instead
         const uint8_t* xp = XLDS && seg_ok ? reinterpret_cast<const uint8_t*>(xs + (size_t)xm * in + (size_t)base * 8)
                                            : zrow;
-        const uint8_t* tbl = lds_cb + (size_t)slot * tbl_bytes;
-        // XM_GTR: the rows' runs of this chunk, issued before the gathers so
-        // their latency runs under them
-        u32x4_t xv[XMODE == XM_GTR ? 16 : 1];
-        if constexpr (XMODE == XM_GTR) {
-          const int blk = c * 64 + lane;
-#pragma unroll
-          for (int u = 0; u < 16; ++u)
-            if (u < M) xv[u] = blk < B ? ldg128(x + (size_t)u * in + (size_t)blk * 8) : u32x4_t{0, 0, 0, 0};
-        }
-        // The activation fragment of block slot tt of the item.
-        auto x_frag = [&](int tt, const u32x4_t (&xt)[XMODE == XM_GTR ? 16 : 1]) -> u32x4_t {
-          if constexpr (XREG) {
-            return xreg[tt];
-          } else if constexpr (XMODE == XM_GTR) {
-            return xt[tt];
-          } else if constexpr (XMODE == XM_LDS) {
-            return *reinterpret_cast<const u32x4_t*>(xp + tt * 16);
-          } else {
-            const u32x4_t xf = ldg128(x + (size_t)xm * in + (size_t)min(base + tt, B - 1) * 8);
-            return seg_ok ? xf : u32x4_t{0, 0, 0, 0};
+        // The item's compute.  xb (M = 1, x in LDS): each lane reads one
+        // 16-byte piece of the chunk's x row (the 16 lanes of a row hold the
+        // segment's 16 fragments, one conflict-free read), and fragment tt is
+        // broadcast from lane tt of each row with DPP instead of 16 LDS reads.
+        auto item = [&](auto xb) {
+          u32x4_t xpiece = {0, 0, 0, 0};
+          if constexpr (decltype(xb)::value) {
+            if (seg_ok) xpiece = *reinterpret_cast<const u32x4_t*>(xs + (size_t)(base + nl) * 8);
           }
-        };
-        auto ids_of = [&](int tt, uint32_t (&id)[S]) {
-#pragma unroll
-          for (int s = 0; s < S; ++s) id[s] = min(extract_id<IdT>(cur[s], tt), kmax);
-        };
-        if constexpr (!SCALED && XMODE != XM_GTR) {
-          // Software pipeline over the item's 16 fragments: the codeword
-          // gathers of fragment tt + GA are issued before fragment tt is
-          // combined (stage sums, roundings and the row-scale product on the
-          // VALU), so each wave's LDS gathers run under its own VALU work
-          // instead of after it.
-          constexpr int GA = decode_gather_ahead<S, LMODE>();
-          const u32x4_t xt_unused[1] = {u32x4_t{0, 0, 0, 0}};
-          WfragRaw<S, LMODE> raw[GA];
-#pragma unroll
-          for (int tt = 0; tt < GA; ++tt) {
-            uint32_t id[S];
-            ids_of(tt, id);
-            raw[tt] = gather_wfrag<S, LMODE>(tbl, id, K);
-          }
-#pragma unroll
-          for (int tt = 0; tt < 16; ++tt) {
-            WfragRaw<S, LMODE> nxt;
-            if (tt + GA < 16) {
-              uint32_t id[S];
-              ids_of(tt + GA, id);
-              nxt = gather_wfrag<S, LMODE>(tbl, id, K);
-            }
-            // keep the next gathers ahead of this fragment's VALU work
-            __builtin_amdgcn_sched_barrier(0);
-            const u32x4_t w = combine_wfrag<S, LMODE, SEM, XDT>(raw[tt % GA], L.active_mask, rs);
-            acc = mfma16<XDT>(x_frag(tt, xt_unused), w, acc);
-            if (tt + GA < 16) raw[tt % GA] = nxt;
-          }
-        } else {
-          // All 16 fragments of the item are gathered before the first MFMA
-          // consumes one, so the LDS latency is paid once per item instead of
-          // once per block.
-          u32x4_t wf[16];
-#pragma unroll
-          for (int tt = 0; tt < 16; ++tt) {
-            uint32_t id[S];
-            ids_of(tt, id);
-            if constexpr (SCALED) wf[tt] = *reinterpret_cast<const u32x4_t*>(tbl + (size_t)id[0] * 16);
-            else wf[tt] = make_wfrag<S, LMODE, SEM, XDT>(tbl, id, K, L.active_mask, rs);
-          }
-          // keep the scheduler from sinking the gathers back next to their MFMAs
-          __builtin_amdgcn_sched_barrier(0);
-          // XM_GTR: rows 0-7, then 8-15, through this wave's 8 KB scratch (piece
-          // p of row r at p ^ r: conflict-free writes, and conflict-free reads
-          // for the 16 lanes of a read pass); each lane reads in the half that
-          // holds its row.  LDS operations of one wave complete in order, so
-          // the second half's writes do not overtake the first half's reads.
-          u32x4_t xt[XMODE == XM_GTR ? 16 : 1];
+          const uint8_t* tbl = lds_cb + (size_t)slot * tbl_bytes;
+          // XM_GTR: the rows' runs of this chunk, issued before the gathers so
+          // their latency runs under them
+          u32x4_t xv[XMODE == XM_GTR ? 16 : 1];
           if constexpr (XMODE == XM_GTR) {
-            uint8_t* sw = xscr + (size_t)wave * kDecodeXScratchBytes;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              if (8 * h < M) {
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                  if (8 * h + u < M)
-                    *reinterpret_cast<u32x4_t*>(sw + u * 1024 + ((lane ^ (8 * h + u)) & 63) * 16) = xv[8 * h + u];
-                if ((xm >> 3) == h) {
-#pragma unroll
-                  for (int tt = 0; tt < 16; ++tt)
-                    xt[tt] = *reinterpret_cast<const u32x4_t*>(sw + (xm - 8 * h) * 1024 + (((16 * q + tt) ^ xm) & 63) * 16);
+            const int blk = c * 64 + lane;
+  #pragma unroll
+            for (int u = 0; u < 16; ++u)
+              if (u < M) xv[u] = blk < B ? ldg128(x + (size_t)u * in + (size_t)blk * 8) : u32x4_t{0, 0, 0, 0};
+          }
+          // The activation fragment of block slot tt of the item.
+          auto x_frag = [&](int tt, const u32x4_t (&xt)[XMODE == XM_GTR ? 16 : 1]) -> u32x4_t {
+            if constexpr (XREG) {
+              return xreg[tt];
+            } else if constexpr (XMODE == XM_GTR) {
+              return xt[tt];
+            } else if constexpr (decltype(xb)::value) {
+              return row_bcast(xpiece, tt);
+            } else if constexpr (XMODE == XM_LDS) {
+              return *reinterpret_cast<const u32x4_t*>(xp + tt * 16);
+            } else {
+              const u32x4_t xf = ldg128(x + (size_t)xm * in + (size_t)min(base + tt, B - 1) * 8);
+              return seg_ok ? xf : u32x4_t{0, 0, 0, 0};
+            }
+          };
+          auto ids_of = [&](int tt, uint32_t (&id)[S]) {
+  #pragma unroll
+            for (int s = 0; s < S; ++s) id[s] = min(extract_id<IdT>(cur[s], tt), kmax);
+          };
+          if constexpr (!SCALED && XMODE != XM_GTR) {
+            // Software pipeline over the item's 16 fragments: the codeword
+            // gathers of fragment tt + GA are issued before fragment tt is
+            // combined (stage sums, roundings and the row-scale product on the
+            // VALU), so each wave's LDS gathers run under its own VALU work
+            // instead of after it.
+            constexpr int GA = decode_gather_ahead<S, LMODE>();
+            const u32x4_t xt_unused[1] = {u32x4_t{0, 0, 0, 0}};
+            WfragRaw<S, LMODE> raw[GA];
+  #pragma unroll
+            for (int tt = 0; tt < GA; ++tt) {
+              uint32_t id[S];
+              ids_of(tt, id);
+              raw[tt] = gather_wfrag<S, LMODE>(tbl, id, K);
+            }
+  #pragma unroll
+            for (int tt = 0; tt < 16; ++tt) {
+              WfragRaw<S, LMODE> nxt;
+              if (tt + GA < 16) {
+                uint32_t id[S];
+                ids_of(tt + GA, id);
+                nxt = gather_wfrag<S, LMODE>(tbl, id, K);
+              }
+              // keep the next gathers ahead of this fragment's VALU work
+              __builtin_amdgcn_sched_barrier(0);
+              const u32x4_t w = combine_wfrag<S, LMODE, SEM, XDT>(raw[tt % GA], L.active_mask, rs);
+              acc = mfma16<XDT>(x_frag(tt, xt_unused), w, acc);
+              if (tt + GA < 16) raw[tt % GA] = nxt;
+            }
+          } else {
+            // All 16 fragments of the item are gathered before the first MFMA
+            // consumes one, so the LDS latency is paid once per item instead of
+            // once per block.
+            u32x4_t wf[16];
+  #pragma unroll
+            for (int tt = 0; tt < 16; ++tt) {
+              uint32_t id[S];
+              ids_of(tt, id);
+              if constexpr (SCALED) wf[tt] = *reinterpret_cast<const u32x4_t*>(tbl + (size_t)id[0] * 16);
+              else wf[tt] = make_wfrag<S, LMODE, SEM, XDT>(tbl, id, K, L.active_mask, rs);
+            }
+            // keep the scheduler from sinking the gathers back next to their MFMAs
+            __builtin_amdgcn_sched_barrier(0);
+            // XM_GTR: rows 0-7, then 8-15, through this wave's 8 KB scratch (piece
+            // p of row r at p ^ r: conflict-free writes, and conflict-free reads
+            // for the 16 lanes of a read pass); each lane reads in the half that
+            // holds its row.  LDS operations of one wave complete in order, so
+            // the second half's writes do not overtake the first half's reads.
+            u32x4_t xt[XMODE == XM_GTR ? 16 : 1];
+            if constexpr (XMODE == XM_GTR) {
+              uint8_t* sw = xscr + (size_t)wave * kDecodeXScratchBytes;
+  #pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                if (8 * h < M) {
+  #pragma unroll
+                  for (int u = 0; u < 8; ++u)
+                    if (8 * h + u < M)
+                      *reinterpret_cast<u32x4_t*>(sw + u * 1024 + ((lane ^ (8 * h + u)) & 63) * 16) = xv[8 * h + u];
+                  if ((xm >> 3) == h) {
+  #pragma unroll
+                    for (int tt = 0; tt < 16; ++tt)
+                      xt[tt] = *reinterpret_cast<const u32x4_t*>(sw + (xm - 8 * h) * 1024 + (((16 * q + tt) ^ xm) & 63) * 16);
+                  }
                 }
               }
             }
+  #pragma unroll
+            for (int tt = 0; tt < 16; ++tt) acc = mfma16<XDT>(x_frag(tt, xt), wf[tt], acc);
           }
-#pragma unroll
-          for (int tt = 0; tt < 16; ++tt) acc = mfma16<XDT>(x_frag(tt, xt), wf[tt], acc);
+        };
+        // (scale-folded tables only: there the item loop has almost no VALU
+        // work, c3 down_proj 12.9 -> 12.0 us; the multi-stage combine is
+        // VALU-bound and the broadcasts made it slower)
+        if constexpr (XMODE == XM_LDS && SCALED) {
+          if (M == 1) item(std::true_type{});
+          else item(std::false_type{});
+        } else {
+          item(std::false_type{});
         }
       }
       if (live && ++ct_c == CPT) {
