@@ -453,6 +453,23 @@ WAL_DEVICE f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) 
 }
 
 
+// 32 x 32 x 16 product: lane l holds A row l % 32 and B column l % 32, k
+// elements 8 (l / 32) .. + 8 of each; D[i][j] is element
+// (i % 4) + 4 (i / 8) of lane j + 32 ((i / 4) % 2).  Same operand registers
+// as mfma16 for twice the flops: measured on gfx950, a VALU instruction of
+// another wave (or of the same one) takes about 1.3 cycles from a stream of
+// these against about 3 from a stream of 16 x 16 x 32 products.
+template <int XDT>
+WAL_DEVICE f32x16_t mfma32(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) {
+  if constexpr (XDT == WAL_F16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+}
+
 // ---- staging from a codebook image ------------------------------------------
 // An image holds, per group, the S x K entries already in their LDS form (the
 // same bytes store_codebook_entry writes), so staging a group is a copy of

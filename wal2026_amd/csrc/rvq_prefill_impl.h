@@ -266,39 +266,54 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
 }
 
 // ---------------------------------------------------------------------------
-// Tall tile: 256 x-rows x 256 weight rows, 12 waves.
+// Tall tile: 256 x-rows x 256 weight rows, 8 waves (two per SIMD, up to 256
+// registers per lane), every wave both dequantising and multiplying.
 //
-// Each dequantised weight feeds BM MFMA rows, so doubling BM halves the
-// dequantisation work per flop.  Register budget: 12 waves are three per
-// SIMD, 168 registers per lane.
-//   * 8 consumer waves (two per SIMD), 2 (M) x 4 (N), each a 128 x 64 output
-//     tile: 128 accumulator registers; the step's four W fragments stay in
-//     registers and the eight x fragments are read one by one next to the
-//     MFMAs that use them.
-//   * 4 producer waves (one per SIMD); thread pt owns weight row pt (all 4
-//     blocks of a k-step) and copies 4 of the x tile's 1024 16-byte pieces.
+// Each dequantised weight feeds 256 MFMA rows, so the dequantisation work per
+// flop is half that of a 128-row tile.  Per k-step (32 columns = 4 blocks):
+//   * wave (wm, wn) of 2 (M) x 4 (N) multiplies its 128 x 64 output tile with
+//     v_mfma_f32_32x32x16 products (4 row blocks x 2 column blocks per k
+//     half): the four W fragments and eight x fragments come from LDS buffer
+//     k & 1; all products of the first k half come before those of the
+//     second, so the two that accumulate into one tile are 8 apart;
+//   * thread t dequantises blocks 2 (t & 1) and 2 (t & 1) + 1 of weight row
+//     t / 2 (bits 2 and 3 of t / 2 swapped, see the bank note below) for step
+//     k + 1 into W buffer (k + 1) & 1, and copies 2 of the x tile's 1024
+//     16-byte pieces.
+// The two waves of a SIMD hide each other's LDS and global latencies.
+// Measured on gfx950 against the alternatives: one dequantising wave beside
+// two multiplying waves per SIMD left the multiplying waves at the barrier
+// more than half the time (the dequantising wave's serial chain set the
+// step); one wave per SIMD with the weights dequantised straight into MFMA
+// registers (no W tile in LDS) lost more to exposed latency than it saved in
+// LDS traffic.  The 32 x 32 product keeps the matrix core busy twice as long
+// per operand read as the 16 x 16 one, and a VALU instruction of the same
+// SIMD takes less of its time (about 1.3 cycles against 3, measured).
+//
 // LDS rows are 64 bytes (one k-step of 16-bit values) with the 16-byte chunk
-// c of row r stored at chunk c ^ ((r >> 1) & 3): a fragment read (lane l:
-// row l % 16, chunk l / 16) is then conflict-free, as with a 96-byte stride,
-// in two thirds of the space.
+// c of row r stored at chunk c ^ f(r), f(r) = bit 2 of r + 2 * bit 4 of r:
+// the fragment reads (lane l: row l % 32, chunk 2 h + l / 32) then run at the
+// rate of sequential reads (measured), and the W and x writes (2 and 4 lanes
+// per row) at the rate of sequential writes.
 // ---------------------------------------------------------------------------
-constexpr int kTallConsumerWaves = 8;
-constexpr int kTallProducerWaves = 4;
-constexpr int kTallThreads = (kTallConsumerWaves + kTallProducerWaves) * 64;
-constexpr int kTallProducerThreads = kTallProducerWaves * 64;
+constexpr int kTallWaves = 8;
+constexpr int kTallThreads = kTallWaves * 64;
 constexpr int TBM = 256;                  // x rows per workgroup tile
 constexpr int kTallRowBytes = PBK * 2;    // 64
 constexpr int kTallTileBytes = 256 * kTallRowBytes;  // one 256-row operand tile (16 KB)
 
 WAL_HOST_DEVICE constexpr int tall_swz(int row, int chunk) { return (chunk ^ ((row >> 1) & 3)) * 16; }
+WAL_HOST_DEVICE constexpr int tall_swz32(int row, int chunk) {
+  return (chunk ^ (((row >> 2) & 1) | ((row >> 3) & 2))) * 16;
+}
 
 template <int S, typename IdT, int LMODE>
 WAL_HOST_DEVICE size_t prefill_tall_lds_bytes(int K, int rshift) {
   return (size_t)4 * kTallTileBytes + ((size_t)prefill_table_entries<S, IdT>(K) * lds_entry_bytes<LMODE>() << rshift);
 }
 
-// Instances whose producer registers fit beside the pipeline (checked with
-// the compiler's resource report: no scratch).
+// Instances whose registers fit 256 per lane without scratch (checked with the
+// compiler's resource report).
 template <int S, typename IdT, int LMODE>
 constexpr bool tall_supported() {
   return prefill_tall_ok(S, LMODE);
@@ -308,8 +323,8 @@ template <int S, typename IdT, int LMODE, int SEM, int XDT>
 __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
                                                                         const uint16_t* __restrict__ x, int64_t M,
                                                                         int n_mt, int rshift) {
-  constexpr int XP = TBM * 4 / kTallProducerThreads;  // 4 x pieces per producer thread per k-step
-  constexpr int NV = sizeof(IdT);
+  constexpr int XP = TBM * 4 / kTallThreads;  // 2 x pieces per thread per k-step
+  constexpr int NV = sizeof(IdT);             // 16-byte index loads per stage per group of 4 k-steps
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* xs = smem;                          // [2][256 rows][64 B]
   uint8_t* ws = smem + 2 * kTallTileBytes;     // [2][256 rows][64 B]
@@ -325,7 +340,7 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
   const int64_t m0 = (int64_t)mt * TBM;
   const int B = L.blocks_per_row;
   const int in = L.in_features;
-  const int nk = B / 4;
+  const int nk = B / 4;  // B % 16 == 0 (host contract): whole k-steps, whole index groups
   const uint32_t kmax = (uint32_t)(K - 1);
 
   constexpr int ESZ = lds_entry_bytes<LMODE>();
@@ -344,78 +359,39 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
           *reinterpret_cast<const u32x4_t*>(compact + (size_t)piece * 16);
     }
   }
-  __syncthreads();
+  __syncthreads();  // table staged (and the compact copy in the W area read)
 
-  if (wave < kTallConsumerWaves) {
-    const int wm = wave >> 2, wn = wave & 3;
-    const int l16 = lane & 15, q = lane >> 4;
-    const int sw = tall_swz(l16, q);  // fragment rows start at multiples of 16
-    const uint8_t* xa = xs + (wm * 128 + l16) * kTallRowBytes + sw;
-    const uint8_t* wb = ws + (wn * 64 + l16) * kTallRowBytes + sw;
-    f32x4_t acc[8][4];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    __syncthreads();  // step 0 produced
-    for (int k = 0; k < nk; ++k) {
-      const int bo = (k & 1) * kTallTileBytes;
-      u32x4_t b[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(wb + bo + j * 16 * kTallRowBytes);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa + bo + i * 16 * kTallRowBytes);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<XDT>(a, b[j], acc[i][j]);
-      }
-      __syncthreads();  // buffer k & 1 read; step k + 1 produced
-    }
-    // Epilogue through LDS (the operand tiles are idle after the last
-    // barrier): per 16-row slice the wave parks its 16 x 64 accumulators in
-    // a private 4 KB area and reads them back one output row per
-    // instruction.  The stores are coalesced, and acc is indexed by
-    // constants only (a loop over it would put the array in scratch memory).
-    float* stage = reinterpret_cast<float*>(smem) + wave * 16 * 64;
-    const int nloc = wn * 64 + lane;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) stage[(4 * q + e) * 64 + j * 16 + l16] = acc[i][j][e];
-      // (one wave's LDS accesses run in order: the reads see these writes,
-      // and the next slice's writes wait for these reads)
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm * 128 + i * 16 + r;
-        const float v = stage[r * 64 + lane];
-        if (m < M && nloc < ti.rows) store_output(E, m, ti.out_row0 + nloc, v);
-      }
-    }
-    return;
-  }
-
-  // ---- producers: thread pt owns weight row pt ----
-  const int pt = tid - kTallConsumerWaves * 64;
-  const uint8_t* lds_lane = lds_cb + (lane & ((1 << rshift) - 1)) * ESZ;
-  const int64_t wr = ti.row0 + (pt < ti.rows ? pt : 0);  // rows past the tile: never stored
+  // ---- dequantisation and x copy: thread tid, weight row pr ----
+  const int q2 = tid >> 1, ph = tid & 1;
+  const int pr = (q2 & ~12) | ((q2 & 4) << 1) | ((q2 & 8) >> 1);
+  const uint8_t* lds_lane = lds_cb + (lane & ((1 << rshift) - 1)) * ESZ;  // this lane's table copy
+  // Rows past the tile dequantise the tile's first row; their outputs are
+  // never stored.
+  const int64_t wr = ti.row0 + (pr < ti.rows ? pr : 0);
   const RowScale rs = make_row_scale<XDT>(load_f(ti.p.row_scale, D.sc_dtype, scale_index(L, wr)));
+  // index planes: one descriptor per stage on the group's base (uniform), the
+  // row in the per-lane offset (rows * B * sizeof(IdT) < 2^31, host check)
   bufrsrc_t idr[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) idr[s] = make_rsrc(ti.p.ids[s]);
   const uint32_t idrow = (uint32_t)(wr * B * (int64_t)sizeof(IdT));
-  // x pieces p = pt + i * 256: row p / 4, 16-byte chunk p % 4
+  // x piece p = tid + i * 512: 16-byte chunk p % 4 of row q = p / 4 with bits
+  // 1 and 2 of q swapped; rows past M read zeros
   const bufrsrc_t xr = make_rsrc(x + m0 * in);
   uint32_t xoff[XP];
   int xdst[XP];
 #pragma unroll
   for (int i = 0; i < XP; ++i) {
-    const int p = pt + i * kTallProducerThreads;
-    const int r = p >> 2, c = p & 3;
+    const int p = tid + i * kTallThreads;
+    const int q = p >> 2, c = p & 3;
+    const int r = (q & ~6) | ((q & 2) << 1) | ((q & 4) >> 1);
     xoff[i] = m0 + r < M ? (uint32_t)((r * in + 8 * c) * 2) : kBufOOB;
-    xdst[i] = r * kTallRowBytes + tall_swz(r, c);
+    xdst[i] = r * kTallRowBytes + tall_swz32(r, c);
   }
-  uint8_t* wd = ws + pt * kTallRowBytes;
+  uint8_t* wd = ws + pr * kTallRowBytes;
+  const int wsw0 = tall_swz32(pr, 2 * ph), wsw1 = tall_swz32(pr, 2 * ph + 1);
+  // Loads are unconditional (a step or group past the end gets an
+  // out-of-range offset and reads zeros), so a step is one basic block.
   auto load_x = [&](int k, u32x4_t (&dst)[XP]) {
     const uint32_t step = k < nk ? (uint32_t)(k * PBK * 2) : kBufOOB;
 #pragma unroll
@@ -428,11 +404,11 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
 #pragma unroll
       for (int v = 0; v < NV; ++v) dst[s][v] = ldbuf128(idr[s], off == kBufOOB ? kBufOOB : off + 16 * v);
   };
-  auto produce = [&](int k, int buf, const u32x4_t (&ids)[S][NV], const u32x4_t (&xv)[XP]) {
-    WfragRaw<S, LMODE> raw[4];
+  // the codewords of this thread's two blocks of step k (index group ids)
+  auto gather = [&](int k, const u32x4_t (&ids)[S][NV], WfragRaw<S, LMODE> (&raw)[2]) {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int t = 4 * (k & 3) + b;  // block inside the 16-block index group
+    for (int b = 0; b < 2; ++b) {
+      const int t = 4 * (k & 3) + 2 * ph + b;  // block inside the 16-block index group
       uint32_t id[S];
 #pragma unroll
       for (int s = 0; s < S; ++s) {
@@ -444,33 +420,108 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
       }
       raw[b] = gather_wfrag_rep<S, LMODE>(lds_lane, id, K, rshift);
     }
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      *reinterpret_cast<u32x4_t*>(wd + buf * kTallTileBytes + tall_swz(pt, b)) =
-          combine_wfrag<S, LMODE, SEM, XDT>(raw[b], L.active_mask, rs);
+  };
+  // the weights of the two blocks and the x pieces of one step into buffer buf
+  auto put = [&](int buf, const WfragRaw<S, LMODE> (&raw)[2], const u32x4_t (&xv)[XP]) {
+    *reinterpret_cast<u32x4_t*>(wd + buf * kTallTileBytes + wsw0) =
+        combine_wfrag<S, LMODE, SEM, XDT>(raw[0], L.active_mask, rs);
+    *reinterpret_cast<u32x4_t*>(wd + buf * kTallTileBytes + wsw1) =
+        combine_wfrag<S, LMODE, SEM, XDT>(raw[1], L.active_mask, rs);
 #pragma unroll
     for (int i = 0; i < XP; ++i) *reinterpret_cast<u32x4_t*>(xs + buf * kTallTileBytes + xdst[i]) = xv[i];
   };
 
-  u32x4_t xq[4][XP];      // x pieces of steps k + 1 .. k + 4 (slot = step & 3)
-  u32x4_t idq[2][S][NV];  // index bytes of two groups of 4 k-steps (slot = group & 1)
-  load_ids(0, idq[0]);
-  load_ids(1, idq[1]);
+  // ---- multiplication: wave (wm, wn), a 128 x 64 output tile ----
+  const int wm = wave >> 2, wn = wave & 3;
+  const int l32 = lane & 31, hk = lane >> 5;
+  // fragment rows start at multiples of 32, so the swizzle of row l32 is that
+  // of every fragment's row
+  const uint8_t* xa = xs + (wm * 128 + l32) * kTallRowBytes;
+  const uint8_t* wb = ws + (wn * 64 + l32) * kTallRowBytes;
+  const int sw0 = tall_swz32(l32, hk), sw1 = tall_swz32(l32, 2 + hk);  // k halves 0 and 1
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  auto multiply = [&](int buf) {
+    const int bo = buf * kTallTileBytes;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int sw = h ? sw1 : sw0;
+      u32x4_t bw[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bw[j] = *reinterpret_cast<const u32x4_t*>(wb + bo + j * 32 * kTallRowBytes + sw);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa + bo + i * 32 * kTallRowBytes + sw);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<XDT>(a, bw[j], acc[i][j]);
+      }
+    }
+  };
+
+  // ---- pipeline: iteration k multiplies step k (buffer k & 1) and produces
+  // step k + 1 into buffer (k + 1) & 1, which every wave finished reading in
+  // iteration k - 1, before the previous barrier; one barrier per step.  x
+  // runs four steps ahead (slot = step & 3), index bytes a group ahead (idc:
+  // the group of the step being produced, idn: the next one).  The loop
+  // takes one index group (4 steps) per trip, so every register-array index
+  // is a constant. ----
+  u32x4_t xq[4][XP];
+  u32x4_t idc[S][NV], idn[S][NV];
+  WfragRaw<S, LMODE> raw[2];
+  load_ids(0, idc);
+  load_ids(1, idn);
 #pragma unroll
   for (int j = 0; j < 4; ++j) load_x(j, xq[j]);
-  produce(0, 0, idq[0], xq[0]);
+  gather(0, idc, raw);
+  put(0, raw, xq[0]);
   load_x(4, xq[0]);
   __syncthreads();  // step 0 produced
-  for (int k0 = 0; k0 < nk; k0 += 8) {
+  for (int g = 0; g < nk / 4; ++g) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int k = k0 + u;
-      if (k >= nk) break;  // uniform
-      const int gs = ((u + 1) >> 2) & 1;
-      produce(k + 1, (u + 1) & 1, idq[gs], xq[(u + 1) & 3]);
+    for (int u = 0; u < 4; ++u) {
+      const int k = 4 * g + u;
+      // step k + 1 is in group g (u < 3) or g + 1 (u == 3); past the end it
+      // reads zeros and writes a buffer nobody reads
+      if (u < 3) gather(k + 1, idc, raw);
+      else gather(k + 1, idn, raw);
+      multiply(u & 1);
+      put((u + 1) & 1, raw, xq[(u + 1) & 3]);
       load_x(k + 5, xq[(u + 1) & 3]);
-      if (((u + 1) & 3) == 3) load_ids(((k + 1) >> 2) + 2, idq[gs]);
-      __syncthreads();
+      if (u == 3) {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int v = 0; v < NV; ++v) idc[s][v] = idn[s][v];
+        load_ids(g + 2, idn);
+      }
+      __syncthreads();  // buffer k & 1 read; step k + 1 produced
+    }
+  }
+
+  // Epilogue through LDS (the operand tiles are idle after the last barrier):
+  // per 32-row slice the wave parks its 32 x 64 accumulators in a private
+  // 8 KB area and reads them back one output row per instruction.  The stores
+  // are coalesced, and acc is indexed by constants only (a loop over it would
+  // put the array in scratch memory).
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * 64;
+  const int nloc = wn * 64 + lane;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) stage[(8 * (e >> 2) + 4 * hk + (e & 3)) * 64 + j * 32 + l32] = acc[i][j][e];
+    // (one wave's LDS accesses run in order: the reads see these writes, and
+    // the next slice's writes wait for these reads)
+    for (int r = 0; r < 32; ++r) {
+      const int64_t m = m0 + wm * 128 + i * 32 + r;
+      const float v = stage[r * 64 + lane];
+      if (m < M && nloc < ti.rows) store_output(E, m, ti.out_row0 + nloc, v);
     }
   }
 }
