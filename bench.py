@@ -37,7 +37,7 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from wal2026_amd import FusedBlockRVQLinears, PackedGroupedBlockRVQLinear, synth  # noqa: E402
+from wal2026_amd import FusedBlockRVQLinears, PackedGroupedBlockRVQLinear, _lib, synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 # linears of a layer that read the same activation, fused into one launch
@@ -351,6 +351,50 @@ def secondary(name: str, layers: int | None, steps: int, warmup: int, dev: torch
     return out
 
 
+def bench_read_ceiling(args, cfg: synth.Config, layers: int, dev: torch.device) -> int:
+    """Time a plain streaming read of the dominant launch's compressed bytes
+    (wal_read_probe: the decode kernel's 16-byte streaming buffer loads, no
+    compute), one cold buffer per layer as in the decode step, at the decode
+    kernel's grid (256 workgroups x 512 threads) and at larger grids, beside the
+    dominant launch itself: the read rate HBM gives this byte count per launch
+    is the practical ceiling for the decode kernel's roofline fraction."""
+    lib = _lib.lib()
+    st = Stack(cfg, layers, dev)
+    dom_name, dom_k, dom_bytes = st.dominant()
+    for layer in st.stack:
+        layer[dom_name](st.xs[dom_k])  # descriptors and codebook images built before timing
+    torch.cuda.synchronize()
+    dom_us = st.launch_us(dom_name)
+    nbytes = (dom_bytes + 15) // 16 * 16
+    gen = torch.Generator(device=dev).manual_seed(0)
+    bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev, generator=gen) for _ in range(layers)]
+    partial = torch.empty(2**16, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+    shapes = [(256, 512), (512, 512), (1024, 512), (2048, 256), (4096, 256)]
+    if args.read_grid:
+        shapes = [(args.read_grid, 512)]
+    rows = []
+    for grid, block in shapes:
+        def launcher(buf, grid=grid, block=block):
+            def run(_x):
+                _lib.check(lib.wal_read_probe(buf.data_ptr(), nbytes, partial.data_ptr(), grid, block,
+                                              stream.cuda_stream))
+            return run
+        us = time_kernel_family([launcher(b) for b in bufs], None, reps=5)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"grid": grid, "block": block, "us": round(us, 3), "GBps": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"read probe {grid} x {block}: {us:.2f} us, {gbs:.0f} GB/s")
+    best = max(rows, key=lambda r: r["frac"])
+    dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
+    print(json.dumps({
+        "mode": "read_ceiling", "config": cfg.name, "launch": dom_name, "bytes_per_launch": nbytes,
+        "layers": layers, "read_probe": rows,
+        "dominant": {"us": round(dom_us, 3), "GBps": round(dom_gbs, 1), "frac": round(dom_gbs / HBM_PEAK_GBS, 4)},
+        "dominant_over_best_read": round(dom_gbs / best["GBps"], 4)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -369,6 +413,11 @@ def main() -> int:
     ap.add_argument("--pmc-summary", default=None,
                     help="rocprofv3 --pmc summary giving the dominant kernel's HBM traffic (default: "
                          "profiles/<decode|prefill>_<config>_<launch>_pmc.txt when it exists)")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="time a plain streaming read of the dominant launch's compressed bytes (wal_read_probe) "
+                         "beside the launch itself: the practical HBM ceiling for this byte count per launch")
+    ap.add_argument("--read-grid", type=int, default=0,
+                    help="with --read-ceiling: only this grid (512 threads per workgroup), for rocprofv3 runs")
     ap.add_argument("--encoder", action="store_true",
                     help="time the encoder's assignment step (wal_rvq_assign) on c3's gate_proj blocks instead")
     args = ap.parse_args()
@@ -390,6 +439,8 @@ def main() -> int:
         cfg = synth.Config(**{**cfg.__dict__, "m": args.m})
     layers = args.layers or cfg.layers
     dev = torch.device("cuda", 0)
+    if args.read_ceiling:
+        return bench_read_ceiling(args, cfg, layers, dev)
     log(f"building {layers} layers of {cfg.name} on {torch.cuda.get_device_name(dev)}")
     st = Stack(cfg, layers, dev)
 

@@ -281,6 +281,16 @@ typedef struct wal_rvq_launch_info {
 int wal_rvq_linear_info(const wal_rvq_layer* layer, int semantics, const void* x, int64_t m, int x_dtype,
                         wal_rvq_launch_info* info);
 
+/* Read-bandwidth probe: reads `bytes` bytes at src (16-byte aligned, a
+ * multiple of 16, below 2^31) with the decode kernel's load form -- 16-byte
+ * buffer loads with the streaming hint, four in flight per lane, grid-stride
+ * over grid workgroups of block threads -- and writes, per wave, the XOR of
+ * the 32-bit words it read to partial[wave] (grid * block / 64 entries; their
+ * XOR is that of every word in the range).  No reference counterpart: the
+ * roofline calibration the bench's read-ceiling mode times against the
+ * decode kernel's compressed bytes. */
+int wal_read_probe(const void* src, int64_t bytes, uint32_t* partial, int grid, int block, void* stream);
+
 /* ---- misc ---------------------------------------------------------------- */
 
 /* Message for the last error on this thread ("" if none). */

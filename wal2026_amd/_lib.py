@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "wal_id_route_reconstruct",
     "wal_rvq_assign",
     "wal_rvq_centroid_sums",
+    "wal_read_probe",
     "wal_last_error",
     "wal_abi_version",
 )
@@ -155,6 +156,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wal_rvq_assign.argtypes = [vp, i64, i32, vp, i64, vp, vp, vp]
     L.wal_rvq_centroid_sums.restype = i32
     L.wal_rvq_centroid_sums.argtypes = [vp, i64, vp, i32, i64, vp, vp, vp]
+    L.wal_read_probe.restype = i32
+    L.wal_read_probe.argtypes = [vp, i64, vp, i32, i32, vp]
 
 
 def lib() -> ctypes.CDLL:

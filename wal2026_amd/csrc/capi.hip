@@ -281,6 +281,28 @@ hipError_t allow_max_lds(const void* kern) {
   return e;
 }
 
+// Read-bandwidth probe: a streaming read of n bytes with the decode kernel's
+// load form (16-byte buffer loads with the streaming hint, four in flight per
+// lane), grid-stride, XOR-reduced so that nothing is optimised away; lane 0 of
+// each wave stores its wave's XOR with a vector store.
+__global__ __launch_bounds__(1024) void read_probe_kernel(const void* src, uint32_t n, uint32_t* partial) {
+  const bufrsrc_t r = make_rsrc(src);
+  const uint32_t stride = gridDim.x * blockDim.x * 16u;
+  u32x4_t acc = {0u, 0u, 0u, 0u};
+  for (uint32_t o = (blockIdx.x * blockDim.x + threadIdx.x) * 16u; o < n; o += 4 * stride) {
+    // pieces past n (and offsets past the resource's range) read zeros
+    const u32x4_t a = ldbuf128_stream(r, o);
+    const u32x4_t b = ldbuf128_stream(r, o + stride < n ? o + stride : kBufOOB);
+    const u32x4_t c = ldbuf128_stream(r, o + 2 * stride < n ? o + 2 * stride : kBufOOB);
+    const u32x4_t d = ldbuf128_stream(r, o + 3 * stride < n ? o + 3 * stride : kBufOOB);
+    acc ^= a ^ b ^ c ^ d;
+  }
+  uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v ^= __shfl_xor(v, m, 64);
+  if ((threadIdx.x & 63) == 0) partial[blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)] = v;
+}
+
 }  // namespace wal
 
 extern "C" {
@@ -605,6 +627,21 @@ int wal_rvq_centroid_sums(const int64_t* ids, int64_t n, const float* blocks, in
   if (k_cb < 1 || k_cb > 0x7fffffff) return fail(WAL_EINVAL, "codebook size must be in [1, 2^31) (got %lld)", (long long)k_cb);
   hipError_t e = launch_centroid_sums(ids, n, blocks, d, (int)k_cb, sums, counts, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_centroid_sums launch");
+}
+
+int wal_read_probe(const void* src, int64_t bytes, uint32_t* partial, int grid, int block, void* stream) {
+  if (!src || !partial) return fail(WAL_EINVAL, "src and partial must be non-NULL");
+  if (!aligned16(src)) return fail(WAL_EINVAL, "src must be 16-byte aligned");
+  if (bytes < 0 || bytes % 16 != 0 || bytes > ((int64_t)1 << 31) - 16)
+    return fail(WAL_EINVAL, "bytes must be a multiple of 16 in [0, 2^31 - 16] (got %lld)", (long long)bytes);
+  if (grid < 1 || block < 64 || block > 1024 || block % 64 != 0)
+    return fail(WAL_EINVAL, "grid must be >= 1 and block a multiple of 64 in [64, 1024] (got %d, %d)", grid, block);
+  if ((int64_t)grid * block * 64 > ((int64_t)1 << 31))
+    return fail(WAL_EINVAL, "grid * block must be at most 2^25 (32-bit offsets, four strides per trip)");
+  hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)grid), dim3((unsigned)block), 0,
+                     reinterpret_cast<hipStream_t>(stream), src, (uint32_t)bytes, partial);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? WAL_OK : hip_fail(e, "read_probe_kernel");
 }
 
 }  // extern "C"
