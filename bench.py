@@ -69,30 +69,41 @@ def linear_bytes(cfg: synth.Config, n: int, k: int) -> int:
     return cfg.num_stages * n * B * ib + G * cfg.num_stages * cfg.codebook_size * cfg.block_size * 2 + n * 2
 
 
-def time_kernel_family(mods, x, reps: int = 3) -> float:
-    """Average GPU duration (us) of one launch of a module (one per layer).
-
-    The launches (one per layer, so each reads weights the previous one did
-    not) are queued behind a GPU sleep, so the host enqueues all of them before
-    the first runs and the HIP event pair recorded around each launch on the
-    launching stream brackets that kernel's own execution, not host latency.
-    """
+def graph_launch_us(fns, reps: int = 5) -> float:
+    """Average GPU duration (us) of one launch among `fns` (one per layer, so
+    each reads weights the previous one did not): the launches are captured in
+    one HIP graph, replayed `reps` times between two HIP events recorded on the
+    stream the graph runs on, and the elapsed time is divided by the launches
+    run.  Inside a graph the launches follow each other with no host gap and no
+    event between them, so this agrees with the profiler's per-dispatch
+    durations (an event pair around each eager launch adds the dispatch
+    latency of the command processor to every one)."""
+    for f in fns:
+        f()  # descriptors, codebook images and allocations outside the graph
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for f in fns:
+            f()
+    torch.cuda.synchronize()
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    times = []
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
     for _ in range(reps):
-        torch.cuda.synchronize()
-        torch.cuda._sleep(20_000_000)  # ~10 ms of GPU spin: the queue fills behind it
-        pairs = []
-        for mod in mods:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            mod(x)
-            b.record(stream)
-            pairs.append((a, b))
-        torch.cuda.synchronize()
-        times.extend(a.elapsed_time(b) * 1000.0 for a, b in pairs)
-    return sum(times) / len(times)
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1000.0 / (len(fns) * reps)
 
 
 def traffic_bytes(path: str):
@@ -300,10 +311,12 @@ class Stack:
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) * 1000.0 / steps, t_issue * 1000.0 / steps
 
-    def launch_us(self, name: str, reps: int = 3) -> float:
+    def launch_us(self, name: str, reps: int = 5) -> float:
+        """Average duration of one `name` launch (graph_launch_us over the layers)."""
         k = next(kk for n, kk, _ in self.fused_launches() if n == name) if name in dict(self.fuse) \
             else self.shape[name][1]
-        return time_kernel_family([layer[name] for layer in self.stack], self.xs[k], reps=reps)
+        x = self.xs[k]
+        return graph_launch_us([(lambda mod=layer[name]: mod(x)) for layer in self.stack], reps=reps)
 
 
 def roofline_of(st: Stack, name: str, nbytes: int, us: float, pmc_summary: str | None) -> dict:
@@ -369,18 +382,17 @@ def bench_read_ceiling(args, cfg: synth.Config, layers: int, dev: torch.device) 
     gen = torch.Generator(device=dev).manual_seed(0)
     bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev, generator=gen) for _ in range(layers)]
     partial = torch.empty(2**16, dtype=torch.int32, device=dev)
-    stream = torch.cuda.current_stream()
     shapes = [(256, 512), (512, 512), (1024, 512), (2048, 256), (4096, 256)]
     if args.read_grid:
         shapes = [(args.read_grid, 512)]
     rows = []
     for grid, block in shapes:
         def launcher(buf, grid=grid, block=block):
-            def run(_x):
+            def run():
                 _lib.check(lib.wal_read_probe(buf.data_ptr(), nbytes, partial.data_ptr(), grid, block,
-                                              stream.cuda_stream))
+                                              torch.cuda.current_stream().cuda_stream))
             return run
-        us = time_kernel_family([launcher(b) for b in bufs], None, reps=5)
+        us = graph_launch_us([launcher(b) for b in bufs], reps=5)
         gbs = nbytes / (us * 1e-6) / 1e9
         rows.append({"grid": grid, "block": block, "us": round(us, 3), "GBps": round(gbs, 1),
                      "frac": round(gbs / HBM_PEAK_GBS, 4)})
@@ -392,6 +404,43 @@ def bench_read_ceiling(args, cfg: synth.Config, layers: int, dev: torch.device) 
         "layers": layers, "read_probe": rows,
         "dominant": {"us": round(dom_us, 3), "GBps": round(dom_gbs, 1), "frac": round(dom_gbs / HBM_PEAK_GBS, 4)},
         "dominant_over_best_read": round(dom_gbs / best["GBps"], 4)}), flush=True)
+    return 0
+
+
+def bench_dense_reference(args, cfg: synth.Config, dev: torch.device) -> int:
+    """Time torch's dense bf16 GEMM (hipBLASLt) at each fused launch shape of
+    the config, x [M, in] @ W^T with W^T a contiguous [in, out] bf16 matrix
+    and no dequantisation: the library rate the prefill kernel is compared
+    with."""
+    st_shapes = []
+    shape = {name: (n, k) for name, n, k in cfg.shapes()}
+    groups = [(f, parts) for f, parts in FUSION_GROUPS if all(p in shape for p in parts)]
+    for fused, parts in groups:
+        st_shapes.append((fused, sum(shape[p][0] for p in parts), shape[parts[0]][1]))
+    fused_parts = {p for _, parts in groups for p in parts}
+    for name, n, k in cfg.shapes():
+        if name not in fused_parts:
+            st_shapes.append((name, n, k))
+    rows = {}
+    for name, n, k in st_shapes:
+        x = torch.randn(cfg.m, k, device=dev, dtype=torch.bfloat16)
+        wt = torch.randn(k, n, device=dev, dtype=torch.bfloat16).contiguous()
+        for _ in range(5):
+            x @ wt
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        a.record()
+        for _ in range(reps):
+            x @ wt
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1000.0 / reps
+        tf = 2.0 * cfg.m * n * k / (us * 1e-6) / 1e12
+        rows[name] = {"m": cfg.m, "n": n, "k": k, "us": round(us, 3), "tflops": round(tf, 1),
+                      "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+        log(f"dense bf16 {name} {cfg.m}x{n}x{k}: {us:.1f} us {tf:.0f} TFLOP/s")
+    print(json.dumps({"mode": "dense_reference", "config": cfg.name, "launches": rows}), flush=True)
     return 0
 
 
@@ -418,6 +467,8 @@ def main() -> int:
                          "beside the launch itself: the practical HBM ceiling for this byte count per launch")
     ap.add_argument("--read-grid", type=int, default=0,
                     help="with --read-ceiling: only this grid (512 threads per workgroup), for rocprofv3 runs")
+    ap.add_argument("--dense-reference", action="store_true",
+                    help="time torch's dense bf16 GEMM (hipBLASLt) at the config's launch shapes, no dequantisation")
     ap.add_argument("--encoder", action="store_true",
                     help="time the encoder's assignment step (wal_rvq_assign) on c3's gate_proj blocks instead")
     args = ap.parse_args()
@@ -441,6 +492,8 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.read_ceiling:
         return bench_read_ceiling(args, cfg, layers, dev)
+    if args.dense_reference:
+        return bench_dense_reference(args, cfg, dev)
     log(f"building {layers} layers of {cfg.name} on {torch.cuda.get_device_name(dev)}")
     st = Stack(cfg, layers, dev)
 
