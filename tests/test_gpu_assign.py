@@ -151,3 +151,35 @@ def test_encoder_on_gpu(gpu_device):
             assert torch.equal(sa, sb)
         for ca, cb in zip(ga.codebooks, gb.codebooks):
             assert torch.equal(ca, cb)
+
+
+def test_cpu_fallbacks_agree_with_the_kernels(gpu_device):
+    """The encoder's host fallbacks (block_vq._nearest and the CPU branch of
+    block_vq._kmeans: the reference's torch expressions, src/block_vq.py:180-227)
+    against the HIP path on the same data.  _nearest picks the same codeword
+    as wal_rvq_assign except where two codewords are within fp32 rounding of
+    each other (its matmul reassociates the dot product), and then its choice
+    is as near in float64; k-means on the host and on the GPU (same Lloyd
+    steps, initial codewords drawn from different generators) reach the same
+    quantisation error within a few percent."""
+    from wal2026_amd.block_vq import _kmeans, _nearest
+
+    b, c = _data(6000, 8, 512, seed=5)
+    ids_cpu, dist_cpu = _nearest(b, c, 1024)
+    ids_gpu, dist_gpu = _assign_to_codebook(b.to(gpu_device), c.to(gpu_device))
+    ids_gpu, dist_gpu = ids_gpu.cpu(), dist_gpu.cpu()
+    same = ids_cpu == ids_gpu
+    assert same.float().mean() > 0.999
+    d64 = ((b.double()[:, None, :] - c.double()[None, :, :]) ** 2).sum(-1)
+    rows = torch.arange(b.shape[0])
+    gap = (d64[rows, ids_cpu] - d64[rows, ids_gpu]).abs()
+    if (~same).any():
+        assert float(gap[~same].max()) <= 1e-5 * float(d64.max())
+    assert torch.allclose(dist_cpu, dist_gpu, rtol=1e-5, atol=1e-5)
+
+    sample, _ = _data(8192, 8, 1, seed=9)
+    cb_cpu = _kmeans(sample, 64, 6, 4096)                      # the host branch
+    cb_gpu = _kmeans(sample.to(gpu_device), 64, 6, 4096).cpu()  # _fit_kmeans on the device
+    err = lambda cb: float(((sample.double()[:, None, :] - cb.double()[None]) ** 2).sum(-1).min(1).values.mean())
+    e_cpu, e_gpu = err(cb_cpu), err(cb_gpu)
+    assert abs(e_cpu - e_gpu) <= 0.05 * max(e_cpu, e_gpu), (e_cpu, e_gpu)
