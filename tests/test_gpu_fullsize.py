@@ -17,7 +17,7 @@ import torch
 
 from _cases import bits, module_buffers_as_encoding, oracle_weight, rel_err
 from oracle import c_oracle
-from wal2026_amd import PackedGroupedBlockRVQLinear, synth
+from wal2026_amd import PackedGroupedBlockRVQLinear, _lib, synth
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -94,6 +94,36 @@ def test_full_prefill_parity_sampled_rows(tile, gpu_device, monkeypatch):
     w_ref = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
     ref = c_oracle.linear_f64(x[rows], w_ref)
     assert rel_err(y[rows], ref) <= TOL
+
+
+def test_full_prefill_fused_gate_up(gpu_device, monkeypatch):
+    """c4's fused gate_up launch (28672 x 4096, M = 2048): 112 weight tiles by
+    8 x tiles, so the 256 x 256 kernel runs 96 tiles whole and splits the last
+    16 into 256 x 128 halves (the round that whole tiles would leave half
+    empty); gate and up are different encodings.  28 sampled rows of y
+    against the oracle, and the fused outputs equal to each linear's own."""
+    from wal2026_amd import FusedBlockRVQLinears
+
+    monkeypatch.delenv("WAL2026_PREFILL_TILE", raising=False)
+    print("[fullsize] prefill c4 gate_up 2048x28672x4096", flush=True)
+    cfg, gate, gen = _layer("c4", 14336, 4096, gpu_device, seed=0)
+    _, up, _ = _layer("c4", 14336, 4096, gpu_device, seed=1)
+    x = synth.make_activation(2048, 4096, cfg.x_dtype, gen)
+    xd = x.to(gpu_device)
+    fused = FusedBlockRVQLinears([gate, up])
+    assert fused.launch_info(xd)["tile_shape"] == "tall"
+    # the fused launch with fp32 outputs (the 2e-3 bar is for fp32 outputs),
+    # then the module's own bf16 outputs
+    c = fused._call_for(xd)
+    y32 = _lib.ops().rvq_linear(xd, c[0], c[1], c[2], None, torch.float32).cpu()
+    yg, yu = fused(xd)
+    rows = torch.randperm(2048, generator=torch.Generator().manual_seed(6))[:24]
+    rows = torch.cat([rows, torch.tensor([0, 255, 256, 2047])])
+    for i, (mod, y) in enumerate(((gate, yg), (up, yu))):
+        w_ref = oracle_weight(module_buffers_as_encoding(mod), cfg.x_dtype)
+        ref = c_oracle.linear_f64(x[rows], w_ref)
+        assert rel_err(y32[rows, 14336 * i:14336 * (i + 1)], ref) <= TOL
+        assert torch.equal(bits(y.contiguous()), bits(mod(xd)))
 
 
 @pytest.mark.parametrize("m", [5, 9, 16])

@@ -145,6 +145,11 @@ LayerArgs make_args(const wal_rvq_layer& L, int kind, uint32_t active_mask) {
   return A;
 }
 
+}  // namespace
+
+namespace wal {
+
+// CUs of the current device (cached per device; 256 when unknown).
 int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
@@ -156,6 +161,10 @@ int device_cu_count() {
   }
   return cached[dev];
 }
+
+}  // namespace wal
+
+namespace {
 
 // LDS form of the codebooks for the MFMA kernels.
 int lds_mode_for(const wal_rvq_layer& L, int sem) {

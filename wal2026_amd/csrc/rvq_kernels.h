@@ -72,6 +72,9 @@ hipError_t launch_image(const LayerArgs& L, const DtypeArgs& D, int sem, int lmo
 // per kernel and device; thread-safe (capi.hip).
 hipError_t allow_max_lds(const void* kern);
 
+// CUs of the current device, cached per device (capi.hip).
+int device_cu_count();
+
 // One-stage decode launches fold the row scale into the staged codebook when
 // every 16-row tile has a single scale value (scale runs of a power of two
 // >= 16 rows).

@@ -319,55 +319,42 @@ constexpr bool tall_supported() {
   return prefill_tall_ok(S, LMODE);
 }
 
-template <int S, typename IdT, int LMODE, int SEM, int XDT>
-__global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
-                                                                        const uint16_t* __restrict__ x, int64_t M,
-                                                                        int n_mt, int rshift) {
+// One tall workgroup's k-loop and epilogue over NB * 128 weight rows of a
+// tile (NB = 2: the whole 256-row tile; NB = 1: the half starting at row
+// wrow0).  Wave (wm, wn) multiplies x rows 128 wm .. + 128 by weight rows
+// 32 NB wn .. + 32 NB; thread t dequantises NB of the 4 blocks of one weight
+// row per k-step.  The table is staged and smem holds [2][x tile] [2][W tile]
+// [table].
+template <int S, typename IdT, int LMODE, int SEM, int XDT, int NB>
+WAL_DEVICE void tall_tile(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E,
+                          const uint16_t* __restrict__ x, int64_t M, const FragTile<S>& ti, int64_t m0, int wrow0,
+                          int rshift, uint8_t* smem) {
   constexpr int XP = TBM * 4 / kTallThreads;  // 2 x pieces per thread per k-step
   constexpr int NV = sizeof(IdT);             // 16-byte index loads per stage per group of 4 k-steps
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int TPR = 4 / NB;                 // threads per weight row
   uint8_t* xs = smem;                          // [2][256 rows][64 B]
-  uint8_t* ws = smem + 2 * kTallTileBytes;     // [2][256 rows][64 B]
+  uint8_t* ws = smem + 2 * kTallTileBytes;     // [2][256 rows][64 B] (NB * 128 rows used)
   uint8_t* lds_cb = smem + 4 * kTallTileBytes;
-
   const int K = L.codebook_size;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int mt = (int)(blockIdx.x % (unsigned)n_mt);
-  const int nt = (int)(blockIdx.x / (unsigned)n_mt);
-  const FragTile<S> ti = get_frag_tile<S>(L, nt);
-  const int64_t m0 = (int64_t)mt * TBM;
   const int B = L.blocks_per_row;
   const int in = L.in_features;
   const int nk = B / 4;  // B % 16 == 0 (host contract): whole k-steps, whole index groups
   const uint32_t kmax = (uint32_t)(K - 1);
-
   constexpr int ESZ = lds_entry_bytes<LMODE>();
-  if (rshift == 0) {
-    stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, ti.p, K, D);
-  } else {
-    uint8_t* compact = ws;  // the W tiles are idle until the first step
-    stage_codebooks<S, LMODE, SEM, XDT>(compact, ti.p, K, D);
-    __syncthreads();
-    const int n16 = prefill_table_entries<S, IdT>(K) * (ESZ / 16);
-    const int nc = 1 << rshift;
-    for (int i = tid; i < n16 * nc; i += kTallThreads) {
-      const int piece = i >> rshift, c = i & (nc - 1);
-      const int e = piece / (ESZ / 16), h = piece - e * (ESZ / 16);
-      *reinterpret_cast<u32x4_t*>(lds_cb + (((e << rshift) + c) * ESZ) + 16 * h) =
-          *reinterpret_cast<const u32x4_t*>(compact + (size_t)piece * 16);
-    }
-  }
-  __syncthreads();  // table staged (and the compact copy in the W area read)
 
-  // ---- dequantisation and x copy: thread tid, weight row pr ----
-  const int q2 = tid >> 1, ph = tid & 1;
-  const int pr = (q2 & ~12) | ((q2 & 4) << 1) | ((q2 & 8) >> 1);
+  // ---- dequantisation and x copy: thread tid, weight row pr, blocks
+  // NB (tid % TPR) .. + NB of every k-step.  Lanes 0-7 and 16-23 (one LDS
+  // write cycle) get rows r0 .. r0 + 3: bits 2 and 3 (NB = 2) or 1 and 2
+  // (NB = 1) of the row index are swapped ----
+  const int q2 = tid / TPR, ph = tid % TPR;
+  const int pr = NB == 2 ? (q2 & ~12) | ((q2 & 4) << 1) | ((q2 & 8) >> 1) : (q2 & ~6) | ((q2 & 2) << 1) | ((q2 & 4) >> 1);
   const uint8_t* lds_lane = lds_cb + (lane & ((1 << rshift) - 1)) * ESZ;  // this lane's table copy
   // Rows past the tile dequantise the tile's first row; their outputs are
   // never stored.
-  const int64_t wr = ti.row0 + (pr < ti.rows ? pr : 0);
+  const int64_t wr = ti.row0 + (wrow0 + pr < ti.rows ? wrow0 + pr : 0);
   const RowScale rs = make_row_scale<XDT>(load_f(ti.p.row_scale, D.sc_dtype, scale_index(L, wr)));
   // index planes: one descriptor per stage on the group's base (uniform), the
   // row in the per-lane offset (rows * B * sizeof(IdT) < 2^31, host check)
@@ -389,7 +376,9 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
     xdst[i] = r * kTallRowBytes + tall_swz32(r, c);
   }
   uint8_t* wd = ws + pr * kTallRowBytes;
-  const int wsw0 = tall_swz32(pr, 2 * ph), wsw1 = tall_swz32(pr, 2 * ph + 1);
+  int wsw[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) wsw[b] = tall_swz32(pr, NB * ph + b);
   // Loads are unconditional (a step or group past the end gets an
   // out-of-range offset and reads zeros), so a step is one basic block.
   auto load_x = [&](int k, u32x4_t (&dst)[XP]) {
@@ -404,11 +393,11 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
 #pragma unroll
       for (int v = 0; v < NV; ++v) dst[s][v] = ldbuf128(idr[s], off == kBufOOB ? kBufOOB : off + 16 * v);
   };
-  // the codewords of this thread's two blocks of step k (index group ids)
-  auto gather = [&](int k, const u32x4_t (&ids)[S][NV], WfragRaw<S, LMODE> (&raw)[2]) {
+  // the codewords of this thread's blocks of step k (index group ids)
+  auto gather = [&](int k, const u32x4_t (&ids)[S][NV], WfragRaw<S, LMODE> (&raw)[NB]) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int t = 4 * (k & 3) + 2 * ph + b;  // block inside the 16-block index group
+    for (int b = 0; b < NB; ++b) {
+      const int t = 4 * (k & 3) + NB * ph + b;  // block inside the 16-block index group
       uint32_t id[S];
 #pragma unroll
       for (int s = 0; s < S; ++s) {
@@ -421,29 +410,29 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
       raw[b] = gather_wfrag_rep<S, LMODE>(lds_lane, id, K, rshift);
     }
   };
-  // the weights of the two blocks and the x pieces of one step into buffer buf
-  auto put = [&](int buf, const WfragRaw<S, LMODE> (&raw)[2], const u32x4_t (&xv)[XP]) {
-    *reinterpret_cast<u32x4_t*>(wd + buf * kTallTileBytes + wsw0) =
-        combine_wfrag<S, LMODE, SEM, XDT>(raw[0], L.active_mask, rs);
-    *reinterpret_cast<u32x4_t*>(wd + buf * kTallTileBytes + wsw1) =
-        combine_wfrag<S, LMODE, SEM, XDT>(raw[1], L.active_mask, rs);
+  // the weights of the thread's blocks and the x pieces of one step into buffer buf
+  auto put = [&](int buf, const WfragRaw<S, LMODE> (&raw)[NB], const u32x4_t (&xv)[XP]) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      *reinterpret_cast<u32x4_t*>(wd + buf * kTallTileBytes + wsw[b]) =
+          combine_wfrag<S, LMODE, SEM, XDT>(raw[b], L.active_mask, rs);
 #pragma unroll
     for (int i = 0; i < XP; ++i) *reinterpret_cast<u32x4_t*>(xs + buf * kTallTileBytes + xdst[i]) = xv[i];
   };
 
-  // ---- multiplication: wave (wm, wn), a 128 x 64 output tile ----
+  // ---- multiplication: wave (wm, wn), a 128 x 32 NB output tile ----
   const int wm = wave >> 2, wn = wave & 3;
   const int l32 = lane & 31, hk = lane >> 5;
   // fragment rows start at multiples of 32, so the swizzle of row l32 is that
   // of every fragment's row
   const uint8_t* xa = xs + (wm * 128 + l32) * kTallRowBytes;
-  const uint8_t* wb = ws + (wn * 64 + l32) * kTallRowBytes;
+  const uint8_t* wb = ws + (wn * 32 * NB + l32) * kTallRowBytes;
   const int sw0 = tall_swz32(l32, hk), sw1 = tall_swz32(l32, 2 + hk);  // k halves 0 and 1
-  f32x16_t acc[4][2];
+  f32x16_t acc[4][NB];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
   auto multiply = [&](int buf) {
@@ -451,14 +440,14 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int sw = h ? sw1 : sw0;
-      u32x4_t bw[2];
+      u32x4_t bw[NB];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bw[j] = *reinterpret_cast<const u32x4_t*>(wb + bo + j * 32 * kTallRowBytes + sw);
+      for (int j = 0; j < NB; ++j) bw[j] = *reinterpret_cast<const u32x4_t*>(wb + bo + j * 32 * kTallRowBytes + sw);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa + bo + i * 32 * kTallRowBytes + sw);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<XDT>(a, bw[j], acc[i][j]);
+        for (int j = 0; j < NB; ++j) acc[i][j] = mfma32<XDT>(a, bw[j], acc[i][j]);
       }
     }
   };
@@ -472,7 +461,7 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
   // is a constant. ----
   u32x4_t xq[4][XP];
   u32x4_t idc[S][NV], idn[S][NV];
-  WfragRaw<S, LMODE> raw[2];
+  WfragRaw<S, LMODE> raw[NB];
   load_ids(0, idc);
   load_ids(1, idn);
 #pragma unroll
@@ -504,26 +493,90 @@ __global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArg
   }
 
   // Epilogue through LDS (the operand tiles are idle after the last barrier):
-  // per 32-row slice the wave parks its 32 x 64 accumulators in a private
-  // 8 KB area and reads them back one output row per instruction.  The stores
-  // are coalesced, and acc is indexed by constants only (a loop over it would
-  // put the array in scratch memory).
-  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * 64;
-  const int nloc = wn * 64 + lane;
+  // per 32-row slice the wave parks its 32 x 32 NB accumulators in a private
+  // area and reads them back one output row per instruction.  The stores are
+  // coalesced, and acc is indexed by constants only (a loop over it would put
+  // the array in scratch memory).
+  constexpr int WC = 32 * NB;  // output columns of a wave
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * WC;
+  const int nloc = wrow0 + wn * WC + lane;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) stage[(8 * (e >> 2) + 4 * hk + (e & 3)) * 64 + j * 32 + l32] = acc[i][j][e];
+      for (int e = 0; e < 16; ++e) stage[(8 * (e >> 2) + 4 * hk + (e & 3)) * WC + j * 32 + l32] = acc[i][j][e];
     // (one wave's LDS accesses run in order: the reads see these writes, and
     // the next slice's writes wait for these reads)
-    for (int r = 0; r < 32; ++r) {
-      const int64_t m = m0 + wm * 128 + i * 32 + r;
-      const float v = stage[r * 64 + lane];
-      if (m < M && nloc < ti.rows) store_output(E, m, ti.out_row0 + nloc, v);
+    if (lane < WC) {
+      for (int r = 0; r < 32; ++r) {
+        const int64_t m = m0 + wm * 128 + i * 32 + r;
+        const float v = stage[r * WC + lane];
+        if (m < M && nloc < ti.rows) store_output(E, m, ti.out_row0 + nloc, v);
+      }
     }
   }
+}
+
+// Grid: blocks [0, n_full * n_mt) take whole 256 x 256 tiles (tile
+// b / n_mt, x tile b % n_mt: the x-tile index fastest, so each XCD's L2 keeps
+// revisiting the same x tiles); the blocks after them split each remaining
+// tile into two 256 x 128 halves.  The host sizes n_full so that the whole
+// tiles fill complete rounds of workgroups and the halves the last one,
+// which whole tiles would leave partly empty.
+template <int S, typename IdT, int LMODE, int SEM, int XDT>
+__global__ __launch_bounds__(kTallThreads) void rvq_prefill_tall_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
+                                                                        const uint16_t* __restrict__ x, int64_t M,
+                                                                        int n_mt, int rshift, int n_full) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* ws = smem + 2 * kTallTileBytes;
+  uint8_t* lds_cb = smem + 4 * kTallTileBytes;
+  const int K = L.codebook_size;
+  const int tid = threadIdx.x;
+  const int bx = (int)blockIdx.x, nfb = n_full * n_mt;
+  int mt, nt, half = -1;  // uniform: the whole workgroup
+  if (bx < nfb) {
+    mt = bx % n_mt;
+    nt = bx / n_mt;
+  } else {
+    const int b2 = bx - nfb, h = b2 / n_mt;
+    mt = b2 - h * n_mt;
+    nt = n_full + (h >> 1);
+    half = h & 1;
+  }
+  const FragTile<S> ti = get_frag_tile<S>(L, nt);
+  if (half > 0 && ti.rows <= 128) return;  // uniform: a second half past the tile's rows
+  const int64_t m0 = (int64_t)mt * TBM;
+
+  constexpr int ESZ = lds_entry_bytes<LMODE>();
+  if (rshift == 0) {
+    stage_codebooks<S, LMODE, SEM, XDT>(lds_cb, ti.p, K, D);
+  } else {
+    uint8_t* compact = ws;  // the W tiles are idle until the first step
+    stage_codebooks<S, LMODE, SEM, XDT>(compact, ti.p, K, D);
+    __syncthreads();
+    const int n16 = prefill_table_entries<S, IdT>(K) * (ESZ / 16);
+    const int nc = 1 << rshift;
+    for (int i = tid; i < n16 * nc; i += kTallThreads) {
+      const int piece = i >> rshift, c = i & (nc - 1);
+      const int e = piece / (ESZ / 16), h = piece - e * (ESZ / 16);
+      *reinterpret_cast<u32x4_t*>(lds_cb + (((e << rshift) + c) * ESZ) + 16 * h) =
+          *reinterpret_cast<const u32x4_t*>(compact + (size_t)piece * 16);
+    }
+  }
+  __syncthreads();  // table staged (and the compact copy in the W area read)
+  if (half < 0) tall_tile<S, IdT, LMODE, SEM, XDT, 2>(L, D, E, x, M, ti, m0, 0, rshift, smem);
+  else tall_tile<S, IdT, LMODE, SEM, XDT, 1>(L, D, E, x, M, ti, m0, 128 * half, rshift, smem);
+}
+
+// How many of the n_tiles weight tiles run whole: those that fill complete
+// rounds of workgroups (one per CU), when the rest, split into halves, fit one
+// more round; otherwise all (a second round of halves would take as long as
+// the partly empty round of whole tiles it replaces).
+inline int tall_full_tiles(int64_t n_tiles, int n_mt, int n_cu) {
+  const int64_t n_full = n_tiles * n_mt / n_cu * n_cu / n_mt;
+  if (n_full < n_tiles && 2 * (n_tiles - n_full) * n_mt <= n_cu) return (int)n_full;
+  return (int)n_tiles;
 }
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT>
@@ -539,9 +592,10 @@ static hipError_t prefill_tall(const LayerArgs& L, const DtypeArgs& D, const Epi
   hipError_t e = allow_max_lds(reinterpret_cast<const void*>(kern));
   if (e != hipSuccess) return e;
   const int n_mt = (int)((M + TBM - 1) / TBM);
-  dim3 grid((unsigned)(L.n_tiles * (int64_t)n_mt));
+  const int n_full = tall_full_tiles(L.n_tiles, n_mt, device_cu_count());
+  dim3 grid((unsigned)(((int64_t)n_full + 2 * (L.n_tiles - n_full)) * n_mt));
   hipLaunchKernelGGL(kern, grid, dim3(kTallThreads), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M, n_mt,
-                     rshift);
+                     rshift, n_full);
   return hipGetLastError();
 }
 
