@@ -8,6 +8,22 @@
  * Every function cites the reference file:line whose arithmetic it restates
  * (paths relative to the reference repository root).
  *
+ * How each function is pinned (tests/test_oracle.py, tests/test_assign_oracle.py):
+ *   conversions          every fp16 pattern; random and special fp32 patterns
+ *                        against numpy and torch casts
+ *   reconstruct_weight   hand-derived golden bits (tests/golden), closed forms
+ *                        (one constant stage, a zero stage, all-zero ids), a
+ *                        float64 bound, the one-hot readout, torch's op sequence
+ *   reconstruct_fast     torch's op sequence, active-stage fixtures
+ *   linear_f64           numpy float64, linearity, the one-hot readout
+ *   triton_rvq_matmul    float64 closed form; power-of-two row scales exact; a
+ *                        planted per-weight scale and a dropped scale caught
+ *   stagewise_linear     torch's op sequence; one-stage closed form
+ *   id_route_weight      hand-derived golden bits (double-rounding ties, an fp16
+ *                        overflow, a subnormal tie); torch's op sequence
+ *   assign               float64 brute force, exact ties, a planted sign error
+ *   centroid_sums        bincount / index_add_ bit for bit; float64 sums
+ *
  * Numbers are passed as raw bit patterns: 16-bit floats as uint16_t, with a
  * dtype tag (OR_F16 / OR_BF16 / OR_F32) saying how to read them.
  */
