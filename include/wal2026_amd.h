@@ -4,9 +4,10 @@
  *
  * This is the drop-in boundary for the reference's DRL-runtime compressed
  * linear forward.  The reference is pure Python (PyTorch + Triton); these entry
- * points are what its Python layer binds (through ctypes)
- * in place of the torch/Triton calls cited on each declaration.  Paths are
- * relative to the reference repository root.
+ * points are what its Python layer binds (through ctypes, or through the
+ * torch operator library built beside this one) in place of the torch/Triton
+ * calls cited on each declaration.  Paths are relative to the reference
+ * repository root.
  *
  * Conventions
  *  - Plain C types only: device pointers are `const void*`, the HIP stream is
