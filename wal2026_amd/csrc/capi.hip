@@ -414,9 +414,21 @@ int wal_rvq_reconstruct(const wal_rvq_layer* layer, int semantics, uint32_t acti
   int sem = 0;
   if (semantics == WAL_RVQ_STAGEWISE) return fail(WAL_EINVAL, "STAGEWISE has no dense weight (it rounds per stage output)");
   if ((rc = resolve_semantics(*layer, semantics, &sem))) return rc;
-  LayerArgs A = make_args(*layer, 0, resolve_mask(*layer, active_stage_mask));
+  const uint32_t mask = resolve_mask(*layer, active_stage_mask);
   DtypeArgs D{layer->id_dtype, layer->codebook_dtype, layer->scale_dtype, out_dtype};
-  hipError_t e = launch_dequant(A, D, sem, w_out, out_dtype, static_cast<hipStream_t>(stream));
+  hipError_t e;
+  const int lmode = lds_mode_for(*layer, sem);
+  const size_t table = (size_t)layer->num_stages * layer->codebook_size * (lmode == LM_F32 ? 32 : 16);
+  if ((sem == SEM_RECON || sem == SEM_FAST) && mfma_layout_ok(*layer, out_dtype, w_out) && table <= kLdsMaxBytes) {
+    // the block-size-8 kernel: 16-row tiles, 64-row tiles when the staged
+    // table is large enough that staging it per 16 rows would cost as much
+    // as the rows' weights
+    LayerArgs A = make_args(*layer, table >= 32 * 1024 ? 1 : 0, mask);
+    e = launch_dequant8(A, D, sem, lmode, w_out, static_cast<hipStream_t>(stream));
+  } else {
+    LayerArgs A = make_args(*layer, 0, mask);
+    e = launch_dequant(A, D, sem, w_out, out_dtype, static_cast<hipStream_t>(stream));
+  }
   return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_reconstruct launch");
 }
 

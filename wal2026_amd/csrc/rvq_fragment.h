@@ -150,14 +150,31 @@ WAL_DEVICE u32x4_t scale_frag_bf16(const u32x4_t& a, uint32_t slo, uint32_t shi)
   return w;
 }
 
-// rne_x(a * rf) for the 8 x-dtype values of a fragment (finite).
-template <int XDT>
+// rne_bf16(a_i * rf) with the sign of every product kept: each bf16 value is
+// widened to fp32 and multiplied (exact: at most 16 significant bits), then
+// the pair is rounded to nearest-even.  For a dense weight, where a -0
+// (a -0 codeword under FAST semantics, or a negative scale) is observable.
+WAL_DEVICE u32x4_t scale_frag_bf16_signed(const u32x4_t& a, float rf) {
+  u32x4_t w;
+#pragma unroll
+  for (int pr = 0; pr < 4; ++pr)
+    w[pr] = pack_bf16(__uint_as_float(a[pr] << 16) * rf, __uint_as_float(a[pr] & 0xffff0000u) * rf);
+  return w;
+}
+
+// rne_x(a * rf) for the 8 x-dtype values of a fragment (finite).  SIGNED_ZERO:
+// keep the sign of a zero product (dense weights); a product's zero sign
+// cannot change a matrix product whose sums start at +0, so the MFMA kernels
+// take the cheaper bf16 form.
+template <int XDT, bool SIGNED_ZERO = false>
 WAL_DEVICE u32x4_t scale_frag(const u32x4_t& a, const RowScale& rs) {
   if constexpr (XDT == WAL_F16) {
     u32x4_t w;
 #pragma unroll
     for (int pr = 0; pr < 4; ++pr) w[pr] = pk_mul_f16(a[pr], rs.r2);
     return w;
+  } else if constexpr (SIGNED_ZERO) {
+    return scale_frag_bf16_signed(a, rs.rf);
   } else {
     return scale_frag_bf16(a, rs.r2, rs.r3);
   }
@@ -232,7 +249,7 @@ WAL_DEVICE void store_codebook_entry(uint8_t* lds, int e, int s, const u32x4_t (
       if constexpr (SEM == SEM_FAST) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = pack_x<XDT>(v[2 * j], v[2 * j + 1]);  // c = rne_x(cb)
-        if (has_ss) o = scale_frag<XDT>(o, make_row_scale<XDT>(ss));            // rne_x(c * rne_x(ss))
+        if (has_ss) o = scale_frag<XDT, true>(o, make_row_scale<XDT>(ss));      // rne_x(c * rne_x(ss))
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -372,7 +389,7 @@ WAL_DEVICE WfragRaw<S, LMODE> gather_wfrag_rep(const uint8_t* lds_lane, const ui
   return r;
 }
 
-template <int S, int LMODE, int SEM, int XDT>
+template <int S, int LMODE, int SEM, int XDT, bool SIGNED_ZERO = false>
 WAL_DEVICE u32x4_t combine_wfrag(const WfragRaw<S, LMODE>& raw, uint32_t active, const RowScale& rs) {
   u32x4_t a;
   if constexpr (LMODE == LM_F32) {
@@ -430,7 +447,7 @@ WAL_DEVICE u32x4_t combine_wfrag(const WfragRaw<S, LMODE>& raw, uint32_t active,
       }
     }
   }
-  return scale_frag<XDT>(a, rs);
+  return scale_frag<XDT, SIGNED_ZERO>(a, rs);
 }
 
 // The 8 weights of one block: gather the S codewords from the staged table,

@@ -65,6 +65,11 @@ hipError_t launch_generic_linear(const LayerArgs& L, const DtypeArgs& D, const E
 // capi.hip decides when those kernels apply (mfma_eligible).
 enum LdsMode : int { LM_A16 = 0, LM_H16 = 1, LM_F32 = 2 };
 
+// Dense weight of a block-size-8 layer the MFMA kernels accept (RECONSTRUCT or
+// FAST, 16-bit output), rvq_dequant8.hip: the codebooks staged in LdsMode
+// form, one workgroup per tile of L's tile kind.
+hipError_t launch_dequant8(const LayerArgs& L, const DtypeArgs& D, int sem, int lmode, void* out, hipStream_t st);
+
 // Codebook image of every group in LdsMode form (rvq_generic.hip).
 hipError_t launch_image(const LayerArgs& L, const DtypeArgs& D, int sem, int lmode, void* dst, hipStream_t st);
 

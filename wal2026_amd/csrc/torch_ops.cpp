@@ -11,6 +11,8 @@
 // descriptor (struct wal_rvq_layer with its plan and codebook image) is built
 // once by the Python layer and passed as its address; it must outlive the
 // call.
+#include <cstdlib>
+
 #include <ATen/ATen.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
@@ -18,6 +20,9 @@
 #include "wal2026_amd.h"
 
 namespace {
+
+// Activation rows from which a prefill call takes the two-pass form.
+constexpr int64_t kTwoPassMinRows = 512;
 
 int dtype_tag(at::ScalarType t) {
   switch (t) {
@@ -28,8 +33,31 @@ int dtype_tag(at::ScalarType t) {
   }
 }
 
+// Whether a prefill call (the library routes it to the fused MFMA kernel)
+// runs as two passes instead: the dense weight, bit for bit the reference's
+// reconstruct_weight / reconstruct_weight_fast (wal_rvq_reconstruct, written
+// at HBM speed), then the library's bf16/fp16 GEMM with the bias in its
+// epilogue -- the reference's own per_group order of work
+// (src/runtime.py:1501-1507), on the GPU.  Measured on MI355X at the c4
+// shapes, the two passes take 0.8-0.9 of the fused kernel's time: torch's
+// GEMM on the natural weight layout runs at about half the bf16 peak, and
+// writing and re-reading the weight costs less than the fused kernel loses to
+// its dequantisation.  WAL2026_PREFILL_TWO_PASS=0 keeps the fused kernel, and
+// so does a forced tile shape (WAL2026_PREFILL_TILE).
+bool prefill_two_pass(const wal_rvq_layer* L, int64_t semantics, const void* x, int64_t m, int xt, int yt) {
+  if (semantics != WAL_RVQ_RECONSTRUCT && semantics != WAL_RVQ_RECONSTRUCT_FAST) return false;
+  if (yt != xt || (xt != WAL_BF16 && xt != WAL_F16) || m < kTwoPassMinRows) return false;
+  const char* f = getenv("WAL2026_PREFILL_TWO_PASS");
+  if (f != nullptr && f[0] == '0') return false;
+  const char* t = getenv("WAL2026_PREFILL_TILE");
+  if (t != nullptr && t[0] != 0) return false;
+  wal_rvq_launch_info info;
+  return wal_rvq_linear_info(L, (int)semantics, x, m, xt, &info) == WAL_OK && info.kernel == WAL_KERNEL_PREFILL;
+}
+
 // y[..., out_features] = x[..., in_features] W^T (+ bias) for the layer at
-// address `layer` (a wal_rvq_layer*): wal_rvq_linear on the current stream.
+// address `layer` (a wal_rvq_layer*): wal_rvq_linear on the current stream,
+// or for a large prefill the dense weight and torch's GEMM (prefill_two_pass).
 at::Tensor rvq_linear(const at::Tensor& x, int64_t layer, int64_t semantics, int64_t stage_mask,
                       const c10::optional<at::Tensor>& bias, c10::optional<at::ScalarType> out_dtype) {
   const wal_rvq_layer* L = reinterpret_cast<const wal_rvq_layer*>(layer);
@@ -61,6 +89,18 @@ at::Tensor rvq_linear(const at::Tensor& x, int64_t layer, int64_t semantics, int
     b = bc.data_ptr();
   }
   hipStream_t st = c10::hip::getCurrentHIPStream(x.device().index()).stream();
+  if (prefill_two_pass(L, semantics, xc.data_ptr(), m, xt, dtype_tag(yt))) {
+    at::Tensor w = at::empty({L->out_features, L->in_features}, x.options());
+    const int rc = wal_rvq_reconstruct(L, (int)semantics, (uint32_t)stage_mask, w.data_ptr(), xt, st);
+    TORCH_CHECK(rc == WAL_OK, "wal2026_amd error ", rc, ": ", wal_last_error());
+    // the bias rounded to the x dtype, added to the fp32 accumulator before
+    // the final rounding (F.linear's order, as the fused kernels do)
+    c10::optional<at::Tensor> bx;
+    if (bc.defined()) bx = bc.to(x.scalar_type());
+    at::Tensor yv = y.view({m, L->out_features});
+    at::linear_out(yv, xc.view({m, L->in_features}), w, bx);
+    return y;
+  }
   const int rc = wal_rvq_linear(L, (int)semantics, (uint32_t)stage_mask, xc.data_ptr(), m, xt, b, bt, y.data_ptr(),
                                 dtype_tag(yt), st);
   TORCH_CHECK(rc == WAL_OK, "wal2026_amd error ", rc, ": ", wal_last_error());
