@@ -19,9 +19,12 @@ sequence timed on this host's cores).
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--m 1]
 
 With --config c4 (M = 2048, two-stage 256-entry codebooks, uint8 indices) the
-same stack runs the prefill kernel instead and the roofline is the bf16 MFMA
+same stack runs the prefill path instead and the roofline is the bf16 MFMA
 one: algorithmic flops (2 M N K per linear) of the dominant launch over its
-measured duration, against the 2.5 PFLOP/s dense peak.
+measured duration, against the 2.5 PFLOP/s dense peak.  From 512 rows the
+torch operator runs a launch as two passes (the dense weight, then torch's
+GEMM); the roofline then also carries the fused prefill kernel's own figures
+(`fused_kernel`, measured with WAL2026_PREFILL_TWO_PASS=0).
 """
 from __future__ import annotations
 
@@ -319,16 +322,50 @@ class Stack:
         return graph_launch_us([(lambda mod=layer[name]: mod(x)) for layer in self.stack], reps=reps)
 
 
+def prefill_fused_us(st: Stack, name: str) -> float:
+    """Duration of one `name` launch with the fused prefill kernel forced
+    (WAL2026_PREFILL_TWO_PASS=0), beside the operator's two-pass choice."""
+    old = os.environ.get("WAL2026_PREFILL_TWO_PASS")
+    os.environ["WAL2026_PREFILL_TWO_PASS"] = "0"
+    try:
+        return st.launch_us(name)
+    finally:
+        if old is None:
+            del os.environ["WAL2026_PREFILL_TWO_PASS"]
+        else:
+            os.environ["WAL2026_PREFILL_TWO_PASS"] = old
+
+
+def pmc_path(kind: str, config: str, name: str, two_pass: bool = False) -> str:
+    return str(ROOT / "profiles" / f"{kind}_{config}_{name}{'_two_pass' if two_pass else ''}_pmc.txt")
+
+
 def roofline_of(st: Stack, name: str, nbytes: int, us: float, pmc_summary: str | None) -> dict:
     cfg = st.cfg
     if cfg.m > 16:
         flops = st.launch_flops(name)
         tflops = flops / (us * 1e-6) / 1e12
-        return {"bound": "mfma", "kernel": f"rvq_prefill_*_kernel, launcher's choice ({name}, {flops} flop)",
-                "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "avg_launch_us": round(us, 3),
-                "algorithmic_flops_per_launch": flops,
-                "traffic": traffic_bytes(pmc_summary) if pmc_summary else None}
+        x = st.xs[next(k for n, k, _ in st.fused_launches() if n == name)]
+        two_pass = st.stack[0][name].launch_info(x).get("two_pass", False)
+        if two_pass:
+            kernel = (f"{name} launch, two passes: rvq_dequant8_kernel (the dense weight, bit-exact) + torch's "
+                      f"bf16 GEMM (hipBLASLt), {flops} flop")
+            pmc_summary = pmc_path("prefill", cfg.name, name, two_pass=True)
+        else:
+            kernel = f"rvq_prefill_*_kernel, launcher's choice ({name}, {flops} flop)"
+        out = {"bound": "mfma", "kernel": kernel, "two_pass": two_pass,
+               "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+               "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "avg_launch_us": round(us, 3),
+               "algorithmic_flops_per_launch": flops,
+               "traffic": traffic_bytes(pmc_summary) if pmc_summary else None}
+        if two_pass:
+            fus = prefill_fused_us(st, name)
+            ftf = flops / (fus * 1e-6) / 1e12
+            out["fused_kernel"] = {"kernel": f"rvq_prefill_*_kernel, launcher's choice ({name})",
+                                   "avg_launch_us": round(fus, 3), "achieved": round(ftf, 1),
+                                   "frac": round(ftf / BF16_PEAK_TFLOPS, 4),
+                                   "traffic": traffic_bytes(pmc_path("prefill", cfg.name, name))}
+        return out
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"bound": "hbm", "kernel": f"rvq_decode_kernel ({name}, {nbytes} compressed bytes)",
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -352,8 +389,7 @@ def secondary(name: str, layers: int | None, steps: int, warmup: int, dev: torch
                        f"{str(cfg.ids_dtype()).replace('torch.', '')} ids, {layers} of {cfg.layers} layers timed, "
                        f"fused, one HIP graph per step, {steps} steps; tok/s over all {cfg.layers} layers",
            "tok_s": round(cfg.m * 1e6 / (us_layer * cfg.layers), 2), "us_per_layer": round(us_layer, 3),
-           "roofline": roofline_of(st, dom_name, dom_bytes, us,
-                                   str(ROOT / "profiles" / f"{kind}_{name}_{dom_name}_pmc.txt"))}
+           "roofline": roofline_of(st, dom_name, dom_bytes, us, pmc_path(kind, name, dom_name))}
     if kind == "decode":
         out["step_hbm_fraction"] = round(cfg.compressed_bytes_per_layer() * layers / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                          4)
@@ -537,7 +573,7 @@ def main() -> int:
     layer_bytes = cfg.compressed_bytes_per_layer()
     prefill = cfg.m > 16
     kind = "prefill" if prefill else "decode"
-    pmc_summary = args.pmc_summary or str(ROOT / "profiles" / f"{kind}_{cfg.name}_{dom_name}_pmc.txt")
+    pmc_summary = args.pmc_summary or pmc_path(kind, cfg.name, dom_name)
     roofline = roofline_of(st, dom_name, dom_bytes, dom_us, pmc_summary)
     n_linears = len(cfg.shapes()) * layers
 

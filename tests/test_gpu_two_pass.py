@@ -1,0 +1,108 @@
+"""The two-pass prefill form of the torch operator, on the GPU: from 512
+activation rows, with an output in x's dtype, the module forward writes the
+dense weight (wal_rvq_reconstruct, bit-exact) and multiplies with torch's GEMM
+-- the reference's own per_group order of work (src/runtime.py:1501-1507).
+
+* when it is taken: launch_info reports it, and the switches that keep the
+  fused prefill kernel (WAL2026_PREFILL_TWO_PASS=0, a forced tile shape, an
+  fp32 output, fewer rows, STAGEWISE) are honoured;
+* parity: bf16 outputs against the oracle's bit-exact weight contracted in
+  float64, max|dy|/max|y| <= 4e-3: the 2e-3 bar of fp32 accumulation plus the
+  output's rounding to bf16 (half an ulp, 2^-9 of max|y|); with the
+  reference's bf16 bias inside F.linear; FAST semantics at every stage cap;
+* against the fused kernel: the same outputs up to one bf16 ulp per element
+  (both accumulate in fp32, in different orders).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from _cases import make_encoding, module_buffers_as_encoding, oracle_weight, rel_err
+from oracle import c_oracle
+from wal2026_amd import PackedGroupedBlockRVQLinear
+
+pytestmark = pytest.mark.gpu
+
+BAR_BF16 = 4e-3
+
+
+def _module(device, strategy="hip_block_rvq", bias=False, S=2, seed=3):
+    enc = make_encoding(1024, 2048, S=S, K=256, group_rows=512, seed=seed)
+    b = (torch.randn(1024, generator=torch.Generator().manual_seed(seed)) * 0.5).to(torch.bfloat16) if bias else None
+    return PackedGroupedBlockRVQLinear(enc, bias=b, matmul_strategy=strategy).to(device), b
+
+
+def _x(m, device, seed=0):
+    return torch.randn(m, 2048, generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16).to(device)
+
+
+@pytest.fixture
+def no_overrides(monkeypatch):
+    for v in ("WAL2026_PREFILL_TWO_PASS", "WAL2026_PREFILL_TILE"):
+        monkeypatch.delenv(v, raising=False)
+    return monkeypatch
+
+
+def test_when_the_two_pass_form_is_taken(gpu_device, no_overrides):
+    mod, _ = _module(gpu_device)
+    assert mod.launch_info(_x(512, gpu_device))["two_pass"] is True
+    assert mod.launch_info(_x(511, gpu_device))["two_pass"] is False
+    assert "two_pass" not in mod.launch_info(_x(16, gpu_device))  # the decode kernel
+    no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "0")
+    assert mod.launch_info(_x(2048, gpu_device))["two_pass"] is False
+    no_overrides.delenv("WAL2026_PREFILL_TWO_PASS")
+    no_overrides.setenv("WAL2026_PREFILL_TILE", "tall")
+    assert mod.launch_info(_x(2048, gpu_device))["two_pass"] is False
+
+
+@pytest.mark.parametrize("m", [512, 700])
+@pytest.mark.parametrize("bias", [False, True], ids=["nobias", "bias"])
+def test_two_pass_parity(m, bias, gpu_device, no_overrides):
+    mod, b = _module(gpu_device, bias=bias)
+    x = _x(m, gpu_device, seed=m)
+    assert mod.launch_info(x)["two_pass"] is True
+    y = mod(x)
+    assert y.dtype == torch.bfloat16 and y.shape == (m, 1024)
+    w = oracle_weight(module_buffers_as_encoding(mod), torch.bfloat16)
+    ref = c_oracle.linear_f64(x.cpu(), w)
+    if b is not None:
+        ref = ref + b.double()  # F.linear's bias: added to the accumulator before the rounding
+    assert rel_err(y, ref) <= BAR_BF16
+
+
+@pytest.mark.parametrize("k", [1, 2])
+def test_two_pass_fast_semantics(k, gpu_device, no_overrides):
+    mod, _ = _module(gpu_device, strategy="per_group_fast", S=2, seed=5)
+    for g in mod.groups:
+        g.set_effective_stages_per_split(k)
+    x = _x(640, gpu_device, seed=k)
+    assert mod.launch_info(x)["two_pass"] is True
+    w = oracle_weight(module_buffers_as_encoding(mod), torch.bfloat16, active=list(range(k)))
+    assert rel_err(mod(x), c_oracle.linear_f64(x.cpu(), w)) <= BAR_BF16
+
+
+def test_two_pass_against_the_fused_kernel(gpu_device, no_overrides):
+    mod, _ = _module(gpu_device, bias=True)
+    x = _x(1024, gpu_device, seed=11)
+    y2 = mod(x).float().cpu()
+    no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "0")
+    assert mod.launch_info(x)["two_pass"] is False
+    y1 = mod(x).float().cpu()
+    # one bf16 ulp of the larger magnitude bounds every difference
+    ulp = torch.maximum(y1.abs(), y2.abs()).clamp_min(1e-30) * 2.0 ** -7
+    assert bool(((y1 - y2).abs() <= ulp).all())
+
+
+def test_fp32_output_keeps_the_fused_kernel(gpu_device, no_overrides):
+    """An fp32 output (the parity tests' form) goes to the fused kernel: the
+    two-pass GEMM would round to bf16 first."""
+    from wal2026_amd import _lib
+
+    mod, _ = _module(gpu_device)
+    x = _x(1024, gpu_device, seed=2)
+    c = mod._call_for(x, False)
+    y = _lib.ops().rvq_linear(x, c[0], c[1], c[2], None, torch.float32)
+    assert y.dtype == torch.float32
+    w = oracle_weight(module_buffers_as_encoding(mod), torch.bfloat16)
+    assert rel_err(y, c_oracle.linear_f64(x.cpu(), w)) <= 2e-3

@@ -107,6 +107,16 @@ at::Tensor rvq_linear(const at::Tensor& x, int64_t layer, int64_t semantics, int
   return y;
 }
 
+// Whether rvq_linear takes the two-pass form for m activation rows of dtype
+// `dtype` (bf16 or fp16 output): the same decision, for reports and tests.
+bool rvq_prefill_two_pass(int64_t layer, int64_t semantics, int64_t m, at::ScalarType dtype) {
+  const wal_rvq_layer* L = reinterpret_cast<const wal_rvq_layer*>(layer);
+  TORCH_CHECK(L != nullptr, "wal2026_amd: null layer descriptor");
+  const int xt = dtype_tag(dtype);
+  // (the launch query reads only the alignment of x: any 16-byte aligned address)
+  return xt >= 0 && prefill_two_pass(L, semantics, reinterpret_cast<const void*>(uintptr_t{4096}), m, xt, xt);
+}
+
 // Tensors on the CPU are refused loudly: the library is the only compute path.
 at::Tensor rvq_linear_cpu(const at::Tensor& x, int64_t, int64_t, int64_t, const c10::optional<at::Tensor>&,
                           c10::optional<at::ScalarType>) {
@@ -118,6 +128,7 @@ at::Tensor rvq_linear_cpu(const at::Tensor& x, int64_t, int64_t, int64_t, const 
 
 TORCH_LIBRARY(wal2026_amd, m) {
   m.def("rvq_linear(Tensor x, int layer, int semantics, int stage_mask, Tensor? bias, ScalarType? out_dtype) -> Tensor");
+  m.def("rvq_prefill_two_pass(int layer, int semantics, int m, ScalarType dtype) -> bool", &rvq_prefill_two_pass);
 }
 
 TORCH_LIBRARY_IMPL(wal2026_amd, CUDA, m) { m.impl("rvq_linear", rvq_linear); }

@@ -11,7 +11,10 @@ Strategy mapping for ``PackedGroupedBlockRVQLinear`` (src/runtime.py:1362-1507):
 * ``per_group``, ``full_weight``, ``chunked_weight``, ``stacked_matmul`` and
   the new ``hip_block_rvq``: the reference's reconstruct_weight arithmetic
   (src/runtime.py:379-414) followed by the contraction, in ONE launch for all
-  row groups (decode kernel for M <= 16, prefill kernel above).
+  row groups (decode kernel for M <= 16, prefill kernel above).  From 512
+  activation rows, with an output in x's dtype, the torch operator runs the
+  reference's own order of work instead -- the dense weight (bit-exact, one
+  launch), then torch's GEMM -- which is faster on MI355X at these shapes.
 * ``per_group_fast``, ``full_weight_fast``: reconstruct_weight_fast arithmetic
   over the active stages (src/runtime.py:568-598).
 * ``triton_block_rvq``: per group, the fused Triton kernel's arithmetic where
@@ -245,6 +248,10 @@ def _launch_info(layer: "_lib.WalLayer", semantics: int, x: Tensor) -> dict:
                    share=info.share, lds_bytes=info.lds_bytes)
     elif info.kernel == _lib.KERNEL_PREFILL:
         out["tile_shape"] = _TILE_NAMES[info.tile_shape]
+        # the torch operator's choice for an output in x's dtype: the dense
+        # weight (wal_rvq_reconstruct) then torch's GEMM, or the fused kernel
+        out["two_pass"] = bool(_lib.ops().rvq_prefill_two_pass(ctypes.addressof(layer), semantics,
+                                                               x_flat.shape[0], x_flat.dtype))
     return out
 
 
