@@ -445,9 +445,10 @@ def bench_read_ceiling(args, cfg: synth.Config, layers: int, dev: torch.device) 
 
 def bench_dense_reference(args, cfg: synth.Config, dev: torch.device) -> int:
     """Time torch's dense bf16 GEMM (hipBLASLt) at each fused launch shape of
-    the config, x [M, in] @ W^T with W^T a contiguous [in, out] bf16 matrix
-    and no dequantisation: the library rate the prefill kernel is compared
-    with."""
+    the config, no dequantisation: the library rate the prefill paths are
+    compared with.  Two weight layouts: W [out, in] as nn.Linear stores it,
+    through F.linear (the two-pass prefill's GEMM), and W^T [in, out]
+    contiguous, through x @ W^T."""
     st_shapes = []
     shape = {name: (n, k) for name, n, k in cfg.shapes()}
     groups = [(f, parts) for f, parts in FUSION_GROUPS if all(p in shape for p in parts)]
@@ -457,25 +458,31 @@ def bench_dense_reference(args, cfg: synth.Config, dev: torch.device) -> int:
     for name, n, k in cfg.shapes():
         if name not in fused_parts:
             st_shapes.append((name, n, k))
-    rows = {}
-    for name, n, k in st_shapes:
-        x = torch.randn(cfg.m, k, device=dev, dtype=torch.bfloat16)
-        wt = torch.randn(k, n, device=dev, dtype=torch.bfloat16).contiguous()
+    def time_us(fn) -> float:
         for _ in range(5):
-            x @ wt
+            fn()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         reps = 20
         a.record()
         for _ in range(reps):
-            x @ wt
+            fn()
         b.record()
         torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1000.0 / reps
-        tf = 2.0 * cfg.m * n * k / (us * 1e-6) / 1e12
-        rows[name] = {"m": cfg.m, "n": n, "k": k, "us": round(us, 3), "tflops": round(tf, 1),
-                      "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
-        log(f"dense bf16 {name} {cfg.m}x{n}x{k}: {us:.1f} us {tf:.0f} TFLOP/s")
+        return a.elapsed_time(b) * 1000.0 / reps
+
+    rows = {}
+    for name, n, k in st_shapes:
+        x = torch.randn(cfg.m, k, device=dev, dtype=torch.bfloat16)
+        w = torch.randn(n, k, device=dev, dtype=torch.bfloat16)
+        wt = w.t().contiguous()
+        row = {"m": cfg.m, "n": n, "k": k}
+        for lay, fn in (("w_out_in", lambda: torch.nn.functional.linear(x, w)), ("wt_in_out", lambda: x @ wt)):
+            us = time_us(fn)
+            tf = 2.0 * cfg.m * n * k / (us * 1e-6) / 1e12
+            row[lay] = {"us": round(us, 3), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+            log(f"dense bf16 {name} {cfg.m}x{n}x{k} ({lay}): {us:.1f} us {tf:.0f} TFLOP/s")
+        rows[name] = row
     print(json.dumps({"mode": "dense_reference", "config": cfg.name, "launches": rows}), flush=True)
     return 0
 
