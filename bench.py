@@ -448,7 +448,11 @@ def bench_dense_reference(args, cfg: synth.Config, dev: torch.device) -> int:
     the config, no dequantisation: the library rate the prefill paths are
     compared with.  Two weight layouts: W [out, in] as nn.Linear stores it,
     through F.linear (the two-pass prefill's GEMM), and W^T [in, out]
-    contiguous, through x @ W^T."""
+    contiguous, through x @ W^T.  The natural layout is also timed with
+    weights N(0, 0.02) (the scale of this build's synthetic codebooks) and
+    with both operands zero: the matrix cores' rate depends on the operands'
+    bit activity (the chip lowers its clock under load), so the zero case
+    bounds what any data reaches."""
     st_shapes = []
     shape = {name: (n, k) for name, n, k in cfg.shapes()}
     groups = [(f, parts) for f, parts in FUSION_GROUPS if all(p in shape for p in parts)]
@@ -482,6 +486,15 @@ def bench_dense_reference(args, cfg: synth.Config, dev: torch.device) -> int:
             tf = 2.0 * cfg.m * n * k / (us * 1e-6) / 1e12
             row[lay] = {"us": round(us, 3), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
             log(f"dense bf16 {name} {cfg.m}x{n}x{k} ({lay}): {us:.1f} us {tf:.0f} TFLOP/s")
+        w_small = (torch.randn(n, k, device=dev) * 0.02).to(torch.bfloat16)
+        x0, w0 = torch.zeros_like(x), torch.zeros_like(w)
+        for data, fn in (("w_out_in_w002", lambda: torch.nn.functional.linear(x, w_small)),
+                         ("w_out_in_zeros", lambda: torch.nn.functional.linear(x0, w0))):
+            us = time_us(fn)
+            tf = 2.0 * cfg.m * n * k / (us * 1e-6) / 1e12
+            row[data] = {"us": round(us, 3), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+            log(f"dense bf16 {name} {cfg.m}x{n}x{k} ({data}): {us:.1f} us {tf:.0f} TFLOP/s")
+        del w_small, x0, w0
         rows[name] = row
     print(json.dumps({"mode": "dense_reference", "config": cfg.name, "launches": rows}), flush=True)
     return 0
