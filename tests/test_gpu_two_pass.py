@@ -82,6 +82,27 @@ def test_two_pass_fast_semantics(k, gpu_device, no_overrides):
     assert rel_err(mod(x), c_oracle.linear_f64(x.cpu(), w)) <= BAR_BF16
 
 
+@pytest.mark.parametrize("layout", ["f16_x", "groups_u16"])
+def test_two_pass_other_layouts(layout, gpu_device, no_overrides):
+    """fp16 activations (the weight written in fp16, torch's fp16 GEMM); and
+    three row groups with 16-bit ids (K = 1024) and a row scale shared by
+    128-row runs."""
+    if layout == "f16_x":
+        enc = make_encoding(1024, 2048, S=2, K=256, group_rows=512, seed=21)
+        dt = torch.float16
+    else:
+        enc = make_encoding(1536, 2048, S=1, K=1024, group_rows=512, scale_run=128, seed=22)
+        dt = torch.bfloat16
+    mod = PackedGroupedBlockRVQLinear(enc, matmul_strategy="hip_block_rvq").to(gpu_device)
+    x = torch.randn(600, 2048, generator=torch.Generator().manual_seed(23)).to(dt).to(gpu_device)
+    assert mod.launch_info(x)["two_pass"] is True
+    y = mod(x)
+    assert y.dtype == dt and y.shape == (600, enc.original_shape[0])
+    w = oracle_weight(module_buffers_as_encoding(mod), dt)
+    # fp16 output: rounding to fp16 is finer than bf16's, so the bf16 bar bounds it too
+    assert rel_err(y, c_oracle.linear_f64(x.cpu(), w)) <= BAR_BF16
+
+
 def test_two_pass_against_the_fused_kernel(gpu_device, no_overrides):
     mod, _ = _module(gpu_device, bias=True)
     x = _x(1024, gpu_device, seed=11)
