@@ -21,10 +21,11 @@ sequence timed on this host's cores).
 With --config c4 (M = 2048, two-stage 256-entry codebooks, uint8 indices) the
 same stack runs the prefill path instead and the roofline is the bf16 MFMA
 one: algorithmic flops (2 M N K per linear) of the dominant launch over its
-measured duration, against the 2.5 PFLOP/s dense peak.  From 512 rows the
-torch operator runs a launch as two passes (the dense weight, then torch's
-GEMM); the roofline then also carries the fused prefill kernel's own figures
-(`fused_kernel`, measured with WAL2026_PREFILL_TWO_PASS=0).
+measured duration, against the 2.5 PFLOP/s dense peak.  Where its cost
+model finds it faster (at M = 2048 for every launch) the torch operator runs
+a launch as two passes (the dense weight, then torch's GEMM); the roofline
+then also carries the fused prefill kernel's own figures (`fused_kernel`,
+measured with WAL2026_PREFILL_TWO_PASS=0).
 """
 from __future__ import annotations
 

@@ -1,11 +1,15 @@
-"""The two-pass prefill form of the torch operator, on the GPU: from 512
-activation rows, with an output in x's dtype, the module forward writes the
-dense weight (wal_rvq_reconstruct, bit-exact) and multiplies with torch's GEMM
--- the reference's own per_group order of work (src/runtime.py:1501-1507).
+"""The two-pass prefill form of the torch operator, on the GPU: for a
+prefill call with an output in x's dtype that its cost model finds faster
+than the fused kernel, the module forward writes the dense weight
+(wal_rvq_reconstruct, bit-exact) and multiplies with torch's GEMM -- the
+reference's own per_group order of work (src/runtime.py:1501-1507).
 
-* when it is taken: launch_info reports it, and the switches that keep the
-  fused prefill kernel (WAL2026_PREFILL_TWO_PASS=0, a forced tile shape, an
-  fp32 output, fewer rows, STAGEWISE) are honoured;
+* when it is taken: launch_info reports it; the cost model's choices at the
+  measured crossovers (a narrow layer at any prefill M, gate_up's shape fused
+  up to 512 rows and two-pass from 768); the switches that keep the fused
+  prefill kernel (WAL2026_PREFILL_TWO_PASS=0, a forced tile shape, an fp32
+  output, decode rows) or force the two passes (WAL2026_PREFILL_TWO_PASS=1)
+  are honoured;
 * parity: bf16 outputs against the oracle's bit-exact weight contracted in
   float64, max|dy|/max|y| <= 4e-3: the 2e-3 bar of fp32 accumulation plus the
   output's rounding to bf16 (half an ulp, 2^-9 of max|y|); with the
@@ -46,8 +50,9 @@ def no_overrides(monkeypatch):
 
 def test_when_the_two_pass_form_is_taken(gpu_device, no_overrides):
     mod, _ = _module(gpu_device)
-    assert mod.launch_info(_x(512, gpu_device))["two_pass"] is True
-    assert mod.launch_info(_x(511, gpu_device))["two_pass"] is False
+    # a 1024-row layer gives the fused kernel 4 weight-row tiles: two passes at any prefill M
+    for m in (17, 511, 512, 2048):
+        assert mod.launch_info(_x(m, gpu_device))["two_pass"] is True, m
     assert "two_pass" not in mod.launch_info(_x(16, gpu_device))  # the decode kernel
     no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "0")
     assert mod.launch_info(_x(2048, gpu_device))["two_pass"] is False
@@ -56,7 +61,26 @@ def test_when_the_two_pass_form_is_taken(gpu_device, no_overrides):
     assert mod.launch_info(_x(2048, gpu_device))["two_pass"] is False
 
 
-@pytest.mark.parametrize("m", [512, 700])
+def test_cost_model_at_the_gate_up_shape(gpu_device, no_overrides):
+    """c4's fused gate_up shape (28672 x 4096): the fused kernel reads 29 MB of
+    indices where the two passes write and read 235 MB of weight, so it is
+    chosen up to 512 rows (measured 95-149 us against 131-175), the two
+    passes from 768 (232 against 272 us)."""
+    from wal2026_amd import synth
+
+    cfg = synth.CONFIGS["c4"]
+    enc = synth.make_encoding(28672, 4096, cfg, synth.generator(0, gpu_device), gpu_device)
+    mod = PackedGroupedBlockRVQLinear(enc, matmul_strategy="hip_block_rvq").to(gpu_device)
+    xb = lambda m: torch.zeros(m, 4096, dtype=torch.bfloat16, device=gpu_device)
+    for m in (64, 256, 512):
+        assert mod.launch_info(xb(m))["two_pass"] is False, m
+    for m in (768, 2048):
+        assert mod.launch_info(xb(m))["two_pass"] is True, m
+    no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "1")
+    assert mod.launch_info(xb(256))["two_pass"] is True
+
+
+@pytest.mark.parametrize("m", [17, 100, 512, 700])
 @pytest.mark.parametrize("bias", [False, True], ids=["nobias", "bias"])
 def test_two_pass_parity(m, bias, gpu_device, no_overrides):
     mod, b = _module(gpu_device, bias=bias)

@@ -15,14 +15,46 @@
 
 #include <ATen/ATen.h>
 #include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
 #include <torch/library.h>
 
 #include "wal2026_amd.h"
 
 namespace {
 
-// Activation rows from which a prefill call takes the two-pass form.
-constexpr int64_t kTwoPassMinRows = 512;
+// Cost model of the two prefill forms (microseconds), from measurements on
+// MI355X at the c4 shapes (M = 64 .. 2048, HIP events):
+//  * fused kernel: rounds of workgroups x k-steps (32 columns each) x the
+//    time of one k-step of the tile shape the library picks: 0.84 (128 x 256
+//    short), 1.22 (256 x 256 tall), 0.76 (256 x 128 wide).  Few weight-row
+//    tiles leave most CUs idle (a 4096-row layer is 16 short tiles per 128 x
+//    rows): down_proj at M = 64 took 249 us fused, 64 us in two passes.
+//  * two passes: the dense weight written at 4.5 TB/s, then torch's GEMM,
+//    which took the weight's read at 4.0 TB/s plus its flops at 1.6 PFLOP/s
+//    (fitted over M = 64 .. 2048, within 20 %), plus 5 us of launches.  At
+//    small M the GEMM streams the weight: fused gate_up (29 MB of indices
+//    instead of 235 MB of weight) wins up to M = 512.
+double fused_prefill_us(const wal_rvq_layer* L, int64_t m, int tile_shape, int n_cu) {
+  const int64_t rows = tile_shape == WAL_TILE_SHORT ? 128 : 256, cols = tile_shape == WAL_TILE_WIDE ? 128 : 256;
+  const double step_us = tile_shape == WAL_TILE_TALL ? 1.22 : (tile_shape == WAL_TILE_WIDE ? 0.76 : 0.84);
+  const int64_t tiles = ((m + rows - 1) / rows) * ((L->out_features + cols - 1) / cols);
+  const int64_t rounds = (tiles + n_cu - 1) / n_cu;
+  return (double)rounds * (double)((L->in_features + 31) / 32) * step_us;
+}
+
+double two_pass_us(const wal_rvq_layer* L, int64_t m) {
+  const double wbytes = 2.0 * (double)L->out_features * (double)L->in_features;
+  const double flops = 2.0 * (double)m * (double)L->out_features * (double)L->in_features;
+  return wbytes / 4.5e6 + wbytes / 4.0e6 + flops / 1.6e9 + 5.0;
+}
+
+int device_cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n < 1)
+    n = 256;
+  return n;
+}
 
 int dtype_tag(at::ScalarType t) {
   switch (t) {
@@ -38,21 +70,26 @@ int dtype_tag(at::ScalarType t) {
 // reconstruct_weight / reconstruct_weight_fast (wal_rvq_reconstruct, written
 // at HBM speed), then the library's bf16/fp16 GEMM with the bias in its
 // epilogue -- the reference's own per_group order of work
-// (src/runtime.py:1501-1507), on the GPU.  Measured on MI355X at the c4
-// shapes, the two passes take 0.8-0.9 of the fused kernel's time: torch's
-// GEMM on the natural weight layout runs at about half the bf16 peak, and
-// writing and re-reading the weight costs less than the fused kernel loses to
-// its dequantisation.  WAL2026_PREFILL_TWO_PASS=0 keeps the fused kernel, and
-// so does a forced tile shape (WAL2026_PREFILL_TILE).
+// (src/runtime.py:1501-1507), on the GPU, whenever the cost model above
+// says it is the faster form (c4, M = 2048: 0.7-0.8 of the fused kernel's
+// time, since torch's GEMM on the natural weight layout runs at about half
+// the bf16 peak and writing and re-reading the weight costs less than the
+// fused kernel loses to its dequantisation).  WAL2026_PREFILL_TWO_PASS=0
+// keeps the fused kernel, and so does a forced tile shape
+// (WAL2026_PREFILL_TILE); WAL2026_PREFILL_TWO_PASS=1 takes the two passes
+// for every eligible call.
 bool prefill_two_pass(const wal_rvq_layer* L, int64_t semantics, const void* x, int64_t m, int xt, int yt) {
   if (semantics != WAL_RVQ_RECONSTRUCT && semantics != WAL_RVQ_RECONSTRUCT_FAST) return false;
-  if (yt != xt || (xt != WAL_BF16 && xt != WAL_F16) || m < kTwoPassMinRows) return false;
+  if (yt != xt || (xt != WAL_BF16 && xt != WAL_F16)) return false;
   const char* f = getenv("WAL2026_PREFILL_TWO_PASS");
   if (f != nullptr && f[0] == '0') return false;
   const char* t = getenv("WAL2026_PREFILL_TILE");
   if (t != nullptr && t[0] != 0) return false;
   wal_rvq_launch_info info;
-  return wal_rvq_linear_info(L, (int)semantics, x, m, xt, &info) == WAL_OK && info.kernel == WAL_KERNEL_PREFILL;
+  if (wal_rvq_linear_info(L, (int)semantics, x, m, xt, &info) != WAL_OK || info.kernel != WAL_KERNEL_PREFILL)
+    return false;
+  if (f != nullptr && f[0] == '1') return true;
+  return two_pass_us(L, m) < fused_prefill_us(L, m, info.tile_shape, device_cu_count());
 }
 
 // y[..., out_features] = x[..., in_features] W^T (+ bias) for the layer at

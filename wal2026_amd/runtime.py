@@ -11,10 +11,11 @@ Strategy mapping for ``PackedGroupedBlockRVQLinear`` (src/runtime.py:1362-1507):
 * ``per_group``, ``full_weight``, ``chunked_weight``, ``stacked_matmul`` and
   the new ``hip_block_rvq``: the reference's reconstruct_weight arithmetic
   (src/runtime.py:379-414) followed by the contraction, in ONE launch for all
-  row groups (decode kernel for M <= 16, prefill kernel above).  From 512
-  activation rows, with an output in x's dtype, the torch operator runs the
+  row groups (decode kernel for M <= 16, prefill kernel above).  For a
+  prefill call with an output in x's dtype, the torch operator runs the
   reference's own order of work instead -- the dense weight (bit-exact, one
-  launch), then torch's GEMM -- which is faster on MI355X at these shapes.
+  launch), then torch's GEMM -- wherever its cost model finds that faster on
+  MI355X (narrow layers at every prefill M, wide ones at large M).
 * ``per_group_fast``, ``full_weight_fast``: reconstruct_weight_fast arithmetic
   over the active stages (src/runtime.py:568-598).
 * ``triton_block_rvq``: per group, the fused Triton kernel's arithmetic where
