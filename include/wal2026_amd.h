@@ -38,7 +38,7 @@ extern "C" {
 #endif
 
 #define WAL_RVQ_MAX_STAGES 8
-#define WAL_ABI_VERSION 3
+#define WAL_ABI_VERSION 4
 
 typedef enum wal_dtype {
   WAL_U8 = 0,   /* index planes, codebook_size <= 256 (src/block_vq.py:160-165) */
@@ -175,6 +175,27 @@ int wal_rvq_linear(const wal_rvq_layer* layer, int semantics,
                    int x_dtype, const void* bias, int bias_dtype, void* y,
                    int y_dtype, void* stream);
 
+/* wal_rvq_linear with a caller workspace (device memory, 16-byte aligned) of
+ * at least wal_rvq_linear_workspace_size bytes (WAL_ESIZE otherwise; NULL
+ * with 0 bytes is wal_rvq_linear).  With it, a prefill call whose output
+ * tiles alone would leave CUs idle (few weight rows at small m: a 4096-row
+ * layer is 16 workgroups at m <= 128) shares each tile's k-steps among
+ * several workgroups, which write fp32 partial sums there; a second launch
+ * adds them in a fixed order, so the result is deterministic (it may differ
+ * from wal_rvq_linear's in the last bits: another fp32 summation order).
+ * Same replacement as wal_rvq_linear (src/runtime.py:1362-1507); the
+ * workspace has no reference counterpart (torch's F.linear sizes its own). */
+int wal_rvq_linear_ws(const wal_rvq_layer* layer, int semantics,
+                      uint32_t active_stage_mask, const void* x, int64_t m,
+                      int x_dtype, const void* bias, int bias_dtype, void* y,
+                      int y_dtype, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* Bytes of workspace wal_rvq_linear_ws uses for these arguments (0: no split;
+ * x is only checked for alignment).  No reference counterpart. */
+int wal_rvq_linear_workspace_size(const wal_rvq_layer* layer, int semantics, const void* x,
+                                  int64_t m, int x_dtype, size_t* bytes);
+
 /* The fused Triton kernel's arithmetic: per block the fp32 sum of all stages
  * is cast to x_dtype, contracted in fp32, and the row scale is applied to the
  * accumulator (not per weight).  Replaces rvq_group_linear_matmul
@@ -264,17 +285,22 @@ typedef struct wal_rvq_launch_info {
   int32_t kernel;       /* WAL_KERNEL_* */
   int32_t x_mode;       /* decode: WAL_XMODE_*; else -1 */
   int32_t table_slots;  /* decode: codebook tables a workgroup keeps in LDS; else -1 */
-  int32_t grid;         /* decode: workgroups; else -1 */
-  int32_t share;        /* decode: 16-row tiles of the largest workgroup share; else -1 */
+  int32_t grid;         /* decode and prefill: workgroups (prefill: of a wal_rvq_linear_ws
+                           call, the tall tile's last-round halves not counted); else -1 */
+  int32_t share;        /* decode: 16-row tiles of the largest workgroup share; prefill:
+                           k-steps (32 columns) of the largest workgroup; else -1 */
   int32_t lds_bytes;    /* decode: dynamic LDS per workgroup; else -1 */
   int32_t tile_shape;   /* prefill: WAL_TILE_*; else -1 */
-  int32_t reserved;
+  int32_t k_splits;     /* prefill: k slices per output tile of a wal_rvq_linear_ws call
+                           with its workspace (wal_rvq_linear: 1); else -1 */
 } wal_rvq_launch_info;
 
-/* What wal_rvq_linear would launch for these arguments, without launching
- * anything (no device memory is read; x is only checked for alignment).  The
- * environment overrides WAL2026_DECODE_XMODE (reg, lds, greg, gtr, global)
- * and WAL2026_PREFILL_TILE (short, tall, wide) apply to both calls; a forced
+/* What wal_rvq_linear (prefill: wal_rvq_linear_ws with its workspace) would
+ * launch for these arguments, without launching anything (no device memory is
+ * read; x is only checked for alignment).  The environment overrides
+ * WAL2026_DECODE_XMODE (reg, lds, greg, gtr, global), WAL2026_PREFILL_TILE
+ * (short, tall, wide) and WAL2026_PREFILL_KSPLIT (1 .. 32 slices of a short
+ * tile's k-steps, with a workspace) apply to every call; a forced
  * x-mode that does not apply to the layer makes both return WAL_EUNSUPPORTED.
  * No reference counterpart: the reference's forward has one code path per
  * strategy (src/runtime.py:1362-1507); this reports which of the library's

@@ -231,7 +231,8 @@ def test_prefill_and_generic_routing(monkeypatch):
     L, _g = _bench_layer([14336], 4096, 2, 256, _lib.U8)
     rc, info = _info(L, 2048)
     assert rc == _lib.OK and info.kernel == _lib.KERNEL_PREFILL and info.tile_shape == _lib.TILE_TALL
-    assert info.x_mode == -1 and info.grid == -1
+    # 56 weight tiles x 8 x tiles, 128 k-steps each, no split
+    assert info.x_mode == -1 and (info.grid, info.share, info.k_splits) == (448, 128, 1)
     monkeypatch.setenv("WAL2026_PREFILL_TILE", "wide")
     rc, info = _info(L, 2048)
     assert rc == _lib.OK and info.tile_shape == _lib.TILE_WIDE
@@ -242,6 +243,50 @@ def test_prefill_and_generic_routing(monkeypatch):
     assert _info(L, 1, x=0x8000008)[1].kernel == _lib.KERNEL_GENERIC
     assert _info(L, 1, semantics=_lib.STAGEWISE)[1].kernel == _lib.KERNEL_GENERIC
     assert _info(L, 0)[1].kernel == _lib.KERNEL_NONE
+
+
+def _ws_size(L, m, x_dtype=_lib.BF16, x=0x8000000):
+    n = ctypes.c_size_t(123)
+    rc = _lib.lib().wal_rvq_linear_workspace_size(ctypes.byref(L), _lib.RECONSTRUCT, x, m, x_dtype, ctypes.byref(n))
+    return rc, n.value
+
+
+def test_prefill_split_k_plan(monkeypatch):
+    """A 4096-row layer at m = 64 is 16 short tiles: with a workspace the
+    planner splits each tile's 448 k-steps 16 ways (one round of 256
+    workgroups, 32 k-steps each) and sizes the fp32 partials; a layer with
+    enough tiles is not split; WAL2026_PREFILL_KSPLIT forces a count."""
+    for v in ("WAL2026_PREFILL_TILE", "WAL2026_PREFILL_KSPLIT"):
+        monkeypatch.delenv(v, raising=False)
+    L, _g = _bench_layer([4096], 14336, 2, 256, _lib.U8)
+    rc, info = _info(L, 64)
+    assert rc == _lib.OK and info.tile_shape == _lib.TILE_SHORT
+    assert (info.grid, info.share, info.k_splits) == (256, 32, 16)
+    assert _ws_size(L, 64) == (_lib.OK, 16 * 64 * 4096 * 4)
+    # 28672 rows: 112 tiles at m = 64, 224 with two slices; 448 tiles at m = 512 (no split)
+    G, _gg = _bench_layer([28672], 4096, 2, 256, _lib.U8)
+    assert (_info(G, 64)[1].k_splits, _info(G, 512)[1].k_splits) == (2, 1)
+    assert _ws_size(G, 512) == (_lib.OK, 0)
+    # decode rows and the generic kernel never split
+    assert _ws_size(L, 16) == (_lib.OK, 0) and _info(L, 16)[1].k_splits == -1
+    assert _ws_size(L, 64, x_dtype=_lib.F32) == (_lib.OK, 0)
+    monkeypatch.setenv("WAL2026_PREFILL_KSPLIT", "3")
+    rc, info = _info(L, 64)
+    assert (info.k_splits, info.grid, info.share) == (3, 48, 8 * 19)  # 56 units of 8 steps: 19 per slice
+    assert _ws_size(L, 64) == (_lib.OK, 3 * 64 * 4096 * 4)
+    monkeypatch.setenv("WAL2026_PREFILL_KSPLIT", "0")
+    assert _info(L, 64)[0] == _lib.EINVAL
+
+
+def test_linear_ws_argument_checks():
+    """wal_rvq_linear_ws refuses a misaligned or too small workspace before
+    any launch (no device memory is touched)."""
+    L, _g = _bench_layer([4096], 14336, 2, 256, _lib.U8)
+    lib = _lib.lib()
+    args = (ctypes.byref(L), _lib.RECONSTRUCT, 0, 0x8000000, 64, _lib.BF16, None, _lib.BF16, 0x9000000, _lib.BF16)
+    assert lib.wal_rvq_linear_ws(*args, 0xA000004, 1 << 30, None) == _lib.EINVAL
+    assert lib.wal_rvq_linear_ws(*args, 0xA000000, 1024, None) == _lib.ESIZE
+    assert b"workspace" in lib.wal_last_error()
 
 
 @pytest.mark.parametrize("mode", ["reg", "lds", "greg", "gtr", "global"])

@@ -5,11 +5,12 @@ than the fused kernel, the module forward writes the dense weight
 reference's own per_group order of work (src/runtime.py:1501-1507).
 
 * when it is taken: launch_info reports it; the cost model's choices at the
-  measured crossovers (a narrow layer at any prefill M, gate_up's shape fused
-  up to 512 rows and two-pass from 768); the switches that keep the fused
-  prefill kernel (WAL2026_PREFILL_TWO_PASS=0, a forced tile shape, an fp32
-  output, decode rows) or force the two passes (WAL2026_PREFILL_TWO_PASS=1)
-  are honoured;
+  measured crossovers (gate_up's shape fused, with its k-steps split at
+  small M, up to 512 rows and two-pass from 768); the switches that keep the
+  fused prefill kernel (WAL2026_PREFILL_TWO_PASS=0, a forced tile shape, an
+  fp32 output, decode rows) or force the two passes
+  (WAL2026_PREFILL_TWO_PASS=1, which the parity tests below use) are
+  honoured;
 * parity: bf16 outputs against the oracle's bit-exact weight contracted in
   float64, max|dy|/max|y| <= 4e-3: the 2e-3 bar of fp32 accumulation plus the
   output's rounding to bf16 (half an ulp, 2^-9 of max|y|); with the
@@ -43,17 +44,18 @@ def _x(m, device, seed=0):
 
 @pytest.fixture
 def no_overrides(monkeypatch):
-    for v in ("WAL2026_PREFILL_TWO_PASS", "WAL2026_PREFILL_TILE"):
+    for v in ("WAL2026_PREFILL_TWO_PASS", "WAL2026_PREFILL_TILE", "WAL2026_PREFILL_KSPLIT"):
         monkeypatch.delenv(v, raising=False)
     return monkeypatch
 
 
 def test_when_the_two_pass_form_is_taken(gpu_device, no_overrides):
     mod, _ = _module(gpu_device)
-    # a 1024-row layer gives the fused kernel 4 weight-row tiles: two passes at any prefill M
-    for m in (17, 511, 512, 2048):
-        assert mod.launch_info(_x(m, gpu_device))["two_pass"] is True, m
+    assert mod.launch_info(_x(2048, gpu_device))["two_pass"] is True
     assert "two_pass" not in mod.launch_info(_x(16, gpu_device))  # the decode kernel
+    no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "1")
+    assert mod.launch_info(_x(17, gpu_device))["two_pass"] is True
+    assert "two_pass" not in mod.launch_info(_x(16, gpu_device))
     no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "0")
     assert mod.launch_info(_x(2048, gpu_device))["two_pass"] is False
     no_overrides.delenv("WAL2026_PREFILL_TWO_PASS")
@@ -72,8 +74,9 @@ def test_cost_model_at_the_gate_up_shape(gpu_device, no_overrides):
     enc = synth.make_encoding(28672, 4096, cfg, synth.generator(0, gpu_device), gpu_device)
     mod = PackedGroupedBlockRVQLinear(enc, matmul_strategy="hip_block_rvq").to(gpu_device)
     xb = lambda m: torch.zeros(m, 4096, dtype=torch.bfloat16, device=gpu_device)
-    for m in (64, 256, 512):
-        assert mod.launch_info(xb(m))["two_pass"] is False, m
+    for m, splits in ((64, 2), (256, 1), (512, 1)):
+        info = mod.launch_info(xb(m))
+        assert info["two_pass"] is False and info["k_splits"] == splits, (m, info)
     for m in (768, 2048):
         assert mod.launch_info(xb(m))["two_pass"] is True, m
     no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "1")
@@ -83,6 +86,7 @@ def test_cost_model_at_the_gate_up_shape(gpu_device, no_overrides):
 @pytest.mark.parametrize("m", [17, 100, 512, 700])
 @pytest.mark.parametrize("bias", [False, True], ids=["nobias", "bias"])
 def test_two_pass_parity(m, bias, gpu_device, no_overrides):
+    no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "1")
     mod, b = _module(gpu_device, bias=bias)
     x = _x(m, gpu_device, seed=m)
     assert mod.launch_info(x)["two_pass"] is True
@@ -97,6 +101,7 @@ def test_two_pass_parity(m, bias, gpu_device, no_overrides):
 
 @pytest.mark.parametrize("k", [1, 2])
 def test_two_pass_fast_semantics(k, gpu_device, no_overrides):
+    no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "1")
     mod, _ = _module(gpu_device, strategy="per_group_fast", S=2, seed=5)
     for g in mod.groups:
         g.set_effective_stages_per_split(k)
@@ -111,6 +116,7 @@ def test_two_pass_other_layouts(layout, gpu_device, no_overrides):
     """fp16 activations (the weight written in fp16, torch's fp16 GEMM); and
     three row groups with 16-bit ids (K = 1024) and a row scale shared by
     128-row runs."""
+    no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "1")
     if layout == "f16_x":
         enc = make_encoding(1024, 2048, S=2, K=256, group_rows=512, seed=21)
         dt = torch.float16
@@ -130,13 +136,24 @@ def test_two_pass_other_layouts(layout, gpu_device, no_overrides):
 def test_two_pass_against_the_fused_kernel(gpu_device, no_overrides):
     mod, _ = _module(gpu_device, bias=True)
     x = _x(1024, gpu_device, seed=11)
+    no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "1")
+    assert mod.launch_info(x)["two_pass"] is True
     y2 = mod(x).float().cpu()
     no_overrides.setenv("WAL2026_PREFILL_TWO_PASS", "0")
+    # the fused kernel unsplit (a split adds its slices' partial sums in
+    # another fp32 order, which near-cancelling outputs show beyond one ulp)
+    no_overrides.setenv("WAL2026_PREFILL_KSPLIT", "1")
     assert mod.launch_info(x)["two_pass"] is False
     y1 = mod(x).float().cpu()
     # one bf16 ulp of the larger magnitude bounds every difference
     ulp = torch.maximum(y1.abs(), y2.abs()).clamp_min(1e-30) * 2.0 ** -7
     assert bool(((y1 - y2).abs() <= ulp).all())
+    # split 8 ways: one ulp plus 1e-4 of max|y| for the summation order
+    no_overrides.setenv("WAL2026_PREFILL_KSPLIT", "8")
+    assert mod.launch_info(x)["k_splits"] == 8
+    y3 = mod(x).float().cpu()
+    bound = torch.maximum(y3.abs(), y2.abs()) * 2.0 ** -7 + 1e-4 * float(y2.abs().max())
+    assert bool(((y3 - y2).abs() <= bound).all())
 
 
 def test_fp32_output_keeps_the_fused_kernel(gpu_device, no_overrides):

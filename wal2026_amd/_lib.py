@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libwal2026_amd.so"
 TORCH_OPS_PATH = Path(__file__).resolve().parent / "_lib" / "libwal2026_amd_torch.so"
 
 MAX_STAGES = 8
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # wal_dtype
 U8, I16, U16, I32 = 0, 1, 2, 3
@@ -38,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "wal_rvq_image_build",
     "wal_rvq_reconstruct",
     "wal_rvq_linear",
+    "wal_rvq_linear_ws",
+    "wal_rvq_linear_workspace_size",
     "wal_rvq_linear_info",
     "wal_rvq_group_linear_matmul",
     "wal_id_route_linear",
@@ -104,7 +106,7 @@ class WalLaunchInfo(ctypes.Structure):
         ("share", ctypes.c_int32),
         ("lds_bytes", ctypes.c_int32),
         ("tile_shape", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("k_splits", ctypes.c_int32),
     ]
 
 
@@ -143,6 +145,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wal_rvq_reconstruct.argtypes = [ctypes.POINTER(WalLayer), i32, u32, vp, i32, vp]
     L.wal_rvq_linear.restype = i32
     L.wal_rvq_linear.argtypes = [ctypes.POINTER(WalLayer), i32, u32, vp, i64, i32, vp, i32, vp, i32, vp]
+    L.wal_rvq_linear_ws.restype = i32
+    L.wal_rvq_linear_ws.argtypes = [ctypes.POINTER(WalLayer), i32, u32, vp, i64, i32, vp, i32, vp, i32, vp, sz, vp]
+    L.wal_rvq_linear_workspace_size.restype = i32
+    L.wal_rvq_linear_workspace_size.argtypes = [ctypes.POINTER(WalLayer), i32, vp, i64, i32, ctypes.POINTER(sz)]
     L.wal_rvq_linear_info.restype = i32
     L.wal_rvq_linear_info.argtypes = [ctypes.POINTER(WalLayer), i32, vp, i64, i32, ctypes.POINTER(WalLaunchInfo)]
     L.wal_rvq_group_linear_matmul.restype = i32

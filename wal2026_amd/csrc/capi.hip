@@ -206,15 +206,19 @@ bool prefill_table_fits(const wal_rvq_layer& L, int sem) {
 
 // Which kernel serves a wal_rvq_linear call, with its launch plan.
 struct Route {
-  int kernel;     // WAL_KERNEL_*
-  DecodePlan dp;  // decode
-  int shape;      // prefill: PrefillShape
+  int kernel;      // WAL_KERNEL_*
+  DecodePlan dp;   // decode
+  int shape;       // prefill: PrefillShape
+  PrefillPlan pp;  // prefill: shape, split, grid
 };
 
-int route_linear(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, int64_t m, Route* r) {
+// allow_split: the call brings a workspace (wal_rvq_linear_ws), so the
+// prefill planner may split the short tile's k-steps.
+int route_linear(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, int64_t m, bool allow_split, Route* r) {
   r->kernel = WAL_KERNEL_GENERIC;
   r->shape = -1;
   r->dp = DecodePlan{-1, -1, -1, -1, 0};
+  r->pp = PrefillPlan{-1, 1, -1, -1};
   if (m == 0) {
     r->kernel = WAL_KERNEL_NONE;
     return WAL_OK;
@@ -239,9 +243,12 @@ int route_linear(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, in
   if (!prefill_table_fits(L, sem)) return WAL_OK;
   const int force = prefill_tile_override();
   if (force == -2) return fail(WAL_EINVAL, "WAL2026_PREFILL_TILE must be short, tall or wide");
+  const int force_ks = prefill_ksplit_override();
+  if (force_ks < 0) return fail(WAL_EINVAL, "WAL2026_PREFILL_KSPLIT must be an integer in 1 .. %d", kMaxKSplit);
   r->kernel = WAL_KERNEL_PREFILL;
-  r->shape = plan_prefill_shape(L.num_stages, lmode, id_bytes(L.id_dtype), m, n_tiles_of(L, 2), device_cu_count(),
-                                force);
+  r->pp = plan_prefill(L.num_stages, lmode, id_bytes(L.id_dtype), m, L.out_features, n_tiles_of(L, 2),
+                       L.blocks_per_row, device_cu_count(), force, allow_split, force_ks);
+  r->shape = r->pp.shape;
   return WAL_OK;
 }
 
@@ -432,8 +439,14 @@ int wal_rvq_reconstruct(const wal_rvq_layer* layer, int semantics, uint32_t acti
   return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_reconstruct launch");
 }
 
-int wal_rvq_linear(const wal_rvq_layer* layer, int semantics, uint32_t active_stage_mask, const void* x, int64_t m,
-                   int x_dtype, const void* bias, int bias_dtype, void* y, int y_dtype, void* stream) {
+// Bytes of the split-K partials a prefill call with this plan writes.
+static size_t splitk_bytes(const wal_rvq_layer& L, int64_t m, const Route& r) {
+  return r.kernel == WAL_KERNEL_PREFILL && r.pp.ksplit > 1 ? (size_t)r.pp.ksplit * (size_t)m * L.out_features * 4 : 0;
+}
+
+static int linear_impl(const wal_rvq_layer* layer, int semantics, uint32_t active_stage_mask, const void* x, int64_t m,
+                int x_dtype, const void* bias, int bias_dtype, void* y, int y_dtype, void* workspace,
+                size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = validate_layer(layer);
   if (rc) return rc;
@@ -454,8 +467,13 @@ int wal_rvq_linear(const wal_rvq_layer* layer, int semantics, uint32_t active_st
   if (layer->image != nullptr && layer->image_tag != WAL_RVQ_IMAGE_TAG(semantics, x_dtype))
     return fail(WAL_EINVAL, "the layer's codebook image was built for tag 0x%x, this call needs 0x%x",
                 layer->image_tag, WAL_RVQ_IMAGE_TAG(semantics, x_dtype));
+  if (workspace != nullptr && !aligned16(workspace)) return fail(WAL_EINVAL, "workspace must be 16-byte aligned");
   Route r;
-  if ((rc = route_linear(*layer, sem, x_dtype, x, m, &r))) return rc;
+  if ((rc = route_linear(*layer, sem, x_dtype, x, m, workspace != nullptr, &r))) return rc;
+  const size_t need = splitk_bytes(*layer, m, r);
+  if (need > 0 && workspace_bytes < need)
+    return fail(WAL_ESIZE, "workspace of %zu bytes, this call needs %zu (wal_rvq_linear_workspace_size)",
+                workspace_bytes, need);
   hipError_t e;
   if (r.kernel == WAL_KERNEL_DECODE) {
     LayerArgs A = make_args(*layer, 0, mask);
@@ -463,13 +481,44 @@ int wal_rvq_linear(const wal_rvq_layer* layer, int semantics, uint32_t active_st
     e = launch_decode(A, D, E, sem, lds_mode_for(*layer, sem), x, (int)m, r.dp, st);
   } else if (r.kernel == WAL_KERNEL_PREFILL) {
     LayerArgs A = make_args(*layer, 2, mask);
-    e = launch_prefill(A, D, E, sem, lds_mode_for(*layer, sem), x, m, r.shape, st);
+    const PrefillSplit sp{need > 0 ? r.pp.ksplit : 1, need > 0 ? static_cast<float*>(workspace) : nullptr};
+    e = launch_prefill(A, D, E, sem, lds_mode_for(*layer, sem), x, m, r.shape, sp, st);
   } else {
     // the generic kernel (STAGEWISE runs every stage: its mask is all stages)
     LayerArgs A = make_args(*layer, 1, sem == SEM_STAGEWISE ? resolve_mask(*layer, 0) : mask);
     e = launch_generic_linear(A, D, E, sem, x, m, st);
   }
   return e == hipSuccess ? WAL_OK : hip_fail(e, "wal_rvq_linear launch");
+}
+
+int wal_rvq_linear(const wal_rvq_layer* layer, int semantics, uint32_t active_stage_mask, const void* x, int64_t m,
+                   int x_dtype, const void* bias, int bias_dtype, void* y, int y_dtype, void* stream) {
+  return linear_impl(layer, semantics, active_stage_mask, x, m, x_dtype, bias, bias_dtype, y, y_dtype, nullptr, 0,
+                     stream);
+}
+
+int wal_rvq_linear_ws(const wal_rvq_layer* layer, int semantics, uint32_t active_stage_mask, const void* x,
+                      int64_t m, int x_dtype, const void* bias, int bias_dtype, void* y, int y_dtype,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  return linear_impl(layer, semantics, active_stage_mask, x, m, x_dtype, bias, bias_dtype, y, y_dtype, workspace,
+                     workspace_bytes, stream);
+}
+
+int wal_rvq_linear_workspace_size(const wal_rvq_layer* layer, int semantics, const void* x, int64_t m, int x_dtype,
+                                  size_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return fail(WAL_EINVAL, "bytes is NULL");
+  *bytes = 0;
+  int rc = validate_layer(layer);
+  if (rc) return rc;
+  if (m < 0) return fail(WAL_EINVAL, "m must be >= 0");
+  if (!is_float_dtype(x_dtype)) return fail(WAL_EINVAL, "bad x dtype %d", x_dtype);
+  int sem = 0;
+  if ((rc = resolve_semantics(*layer, semantics, &sem))) return rc;
+  Route r;
+  if ((rc = route_linear(*layer, sem, x_dtype, x, m, true, &r))) return rc;
+  *bytes = splitk_bytes(*layer, m, r);
+  return WAL_OK;
 }
 
 int wal_rvq_linear_info(const wal_rvq_layer* layer, int semantics, const void* x, int64_t m, int x_dtype,
@@ -483,16 +532,16 @@ int wal_rvq_linear_info(const wal_rvq_layer* layer, int semantics, const void* x
   int sem = 0;
   if ((rc = resolve_semantics(*layer, semantics, &sem))) return rc;
   Route r;
-  if ((rc = route_linear(*layer, sem, x_dtype, x, m, &r))) return rc;
+  if ((rc = route_linear(*layer, sem, x_dtype, x, m, true, &r))) return rc;
   info->kernel = r.kernel;
-  const bool dec = r.kernel == WAL_KERNEL_DECODE;
+  const bool dec = r.kernel == WAL_KERNEL_DECODE, pre = r.kernel == WAL_KERNEL_PREFILL;
   info->x_mode = dec ? r.dp.xmode : -1;
   info->table_slots = dec ? r.dp.nslots : -1;
-  info->grid = dec ? r.dp.grid : -1;
-  info->share = dec ? r.dp.share : -1;
+  info->grid = dec ? r.dp.grid : (pre ? r.pp.grid : -1);
+  info->share = dec ? r.dp.share : (pre ? r.pp.ksteps : -1);
   info->lds_bytes = dec ? (int32_t)r.dp.lds : -1;
-  info->tile_shape = r.kernel == WAL_KERNEL_PREFILL ? r.shape : -1;
-  info->reserved = 0;
+  info->tile_shape = pre ? r.shape : -1;
+  info->k_splits = pre ? r.pp.ksplit : -1;
   return WAL_OK;
 }
 

@@ -262,6 +262,31 @@ hipError_t launch_generic_linear(const LayerArgs& L, const DtypeArgs& D, const E
   }
 }
 
+// ---------------------------------------------------------------------------
+// Split-K reduction of the 128 x 256 prefill tile: one thread per output,
+// the slices' fp32 partials summed in ascending slice order from +0 (so the
+// result does not depend on the order the slices ran in), then the same
+// epilogue as an unsplit launch (bias, rounding to y's dtype).  The partial
+// rows have the stride of y (E.ldy).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rvq_splitk_reduce_kernel(const float* __restrict__ part, int ksplit, int64_t M,
+                                                                EpilogueArgs E) {
+  const int64_t N = E.ldy;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * N) return;
+  const int64_t slice = M * N;
+  float v = 0.0f;
+  for (int s = 0; s < ksplit; ++s) v += part[(int64_t)s * slice + i];
+  store_output(E, i / N, i - (i / N) * N, v);
+}
+
+hipError_t launch_splitk_reduce(const float* part, int ksplit, int64_t M, const EpilogueArgs& E, hipStream_t st) {
+  const int64_t n = M * E.ldy;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(rvq_splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, ksplit, M,
+                     E);
+  return hipGetLastError();
+}
 
 // ---------------------------------------------------------------------------
 // Codebook image: every entry of every stage of every group converted once

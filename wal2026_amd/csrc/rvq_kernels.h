@@ -90,9 +90,21 @@ inline __host__ __device__ bool decode_scaled_tables(int num_stages, int scale_r
 template <int XDT, typename IdT>
 hipError_t decode_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
                         const void* x, int M, const DecodePlan& P, hipStream_t st);
+// Split-K of the 128 x 256 prefill tile: ksplit slices of the k-steps, fp32
+// partials in part ([ksplit][M][out_features], caller memory), summed by
+// launch_splitk_reduce.  ksplit == 1 (or part == nullptr): no split.
+struct PrefillSplit {
+  int ksplit;
+  float* part;
+};
+
 template <int XDT, typename IdT>
 hipError_t prefill_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                         const void* x, int64_t M, int shape, hipStream_t st);
+                         const void* x, int64_t M, int shape, const PrefillSplit& sp, hipStream_t st);
+
+// y[m, n] = epilogue(sum over s = 0 .. ksplit-1 of part[s][m][n]), slices in
+// ascending order (rvq_generic.hip).
+hipError_t launch_splitk_reduce(const float* part, int ksplit, int64_t M, const EpilogueArgs& E, hipStream_t st);
 
 // One explicit instantiation per (activation dtype, index width), each in its
 // own translation unit (rvq_decode_<x>_<ids>.hip, rvq_prefill_<x>_<ids>.hip);
@@ -106,13 +118,13 @@ extern template hipError_t decode_entry<WAL_F16, uint8_t>(const LayerArgs&, cons
 extern template hipError_t decode_entry<WAL_F16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
     int, int, const void*, int, const DecodePlan&, hipStream_t);
 extern template hipError_t prefill_entry<WAL_BF16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-    int, int, const void*, int64_t, int, hipStream_t);
+    int, int, const void*, int64_t, int, const PrefillSplit&, hipStream_t);
 extern template hipError_t prefill_entry<WAL_BF16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-    int, int, const void*, int64_t, int, hipStream_t);
+    int, int, const void*, int64_t, int, const PrefillSplit&, hipStream_t);
 extern template hipError_t prefill_entry<WAL_F16, uint8_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-    int, int, const void*, int64_t, int, hipStream_t);
+    int, int, const void*, int64_t, int, const PrefillSplit&, hipStream_t);
 extern template hipError_t prefill_entry<WAL_F16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&,
-    int, int, const void*, int64_t, int, hipStream_t);
+    int, int, const void*, int64_t, int, const PrefillSplit&, hipStream_t);
 
 // Nearest codeword of n blocks of d floats (d in {1, 2, 4, 8, 16, 32}),
 // rvq_assign.hip.
@@ -134,16 +146,17 @@ inline hipError_t launch_decode(const LayerArgs& L, const DtypeArgs& D, const Ep
               : decode_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, P, st);
 }
 
-// shape: PrefillShape from plan_prefill_shape.
+// shape: PrefillShape from plan_prefill_shape; sp: split-K of the short tile.
 inline hipError_t launch_prefill(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem,
-                                 int lds_mode, const void* x, int64_t M, int shape, hipStream_t st) {
+                                 int lds_mode, const void* x, int64_t M, int shape, const PrefillSplit& sp,
+                                 hipStream_t st) {
   if (L.n_tiles == 0 || M == 0) return hipSuccess;
   const bool wide = D.id_dtype != WAL_U8;
   if (D.x_dtype == WAL_BF16)
-    return wide ? prefill_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, shape, st)
-                : prefill_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, shape, st);
-  return wide ? prefill_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, shape, st)
-              : prefill_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, shape, st);
+    return wide ? prefill_entry<WAL_BF16, uint16_t>(L, D, E, sem, lds_mode, x, M, shape, sp, st)
+                : prefill_entry<WAL_BF16, uint8_t>(L, D, E, sem, lds_mode, x, M, shape, sp, st);
+  return wide ? prefill_entry<WAL_F16, uint16_t>(L, D, E, sem, lds_mode, x, M, shape, sp, st)
+              : prefill_entry<WAL_F16, uint8_t>(L, D, E, sem, lds_mode, x, M, shape, sp, st);
 }
 
 }  // namespace wal

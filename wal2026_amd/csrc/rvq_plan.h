@@ -152,23 +152,76 @@ inline int prefill_tile_override() {
   return -2;
 }
 
-// Tile shape of a prefill launch: 128 x 256 (short), 256 x 256 (tall) or
-// 256 x 128 (wide) x rows by weight rows.  One workgroup per CU, and every
-// shape's workgroup runs the same k-steps: cost = rounds of workgroups x time
-// per k-step, measured at c4 (gfx950) as 0.84 (short), 1.22 (tall), 0.76
-// (wide) us.  A forced shape the instance lacks falls back to short.
-inline int plan_prefill_shape(int S, int lmode, int id_bytes, int64_t M, int n_tiles256, int n_cu, int force) {
+// Split-K of the short tile: at most this many slices, each at least one
+// unit of 8 k-steps (the kernel's kSplitUnit).
+constexpr int kMaxKSplit = 32;
+constexpr int kKSplitUnit = 8;
+
+// WAL2026_PREFILL_KSPLIT (a slice count for every split-capable call, 1 = no
+// split), or 0 (planner's choice); -1 for a bad value.
+inline int prefill_ksplit_override() {
+  const char* f = getenv("WAL2026_PREFILL_KSPLIT");
+  if (f == nullptr || *f == 0) return 0;
+  const int v = atoi(f);
+  return v >= 1 && v <= kMaxKSplit ? v : -1;
+}
+
+struct PrefillPlan {
+  int shape;   // PrefillShape
+  int ksplit;  // k slices of the short tile (1: none)
+  int grid;    // workgroups of the prefill kernel
+  int ksteps;  // k-steps of the largest workgroup
+};
+
+// Tile shape (and split) of a prefill launch: 128 x 256 (short), 256 x 256
+// (tall) or 256 x 128 (wide) x rows by weight rows, one workgroup per CU.
+// Cost = rounds of workgroups x k-steps per workgroup x time per k-step,
+// measured at c4 (gfx950) as 0.84 (short), 1.22 (tall), 0.76 (wide) us.  With
+// split (a caller workspace), the short tile's output tiles can share their
+// k-steps among ksplit workgroups when the tiles alone leave CUs idle (a
+// 4096-row layer at M <= 128 is 16 workgroups), adding one pass that sums the
+// fp32 partials (read at about 3 TB/s).  A forced shape the instance lacks
+// falls back to short; force_ks > 0 forces the slice count of a short tile.
+inline PrefillPlan plan_prefill(int S, int lmode, int id_bytes, int64_t M, int64_t N, int n_tiles256,
+                                int blocks_per_row, int n_cu, int force, bool allow_split, int force_ks) {
   const bool can_tall = prefill_tall_ok(S, lmode), can_wide = prefill_wide_ok(S, lmode, id_bytes);
-  if (force == PS_SHORT) return PS_SHORT;
-  if (force == PS_TALL) return can_tall ? PS_TALL : PS_SHORT;
-  if (force == PS_WIDE) return can_wide ? PS_WIDE : PS_SHORT;
-  if (M <= 128) return PS_SHORT;
   const int64_t cu = n_cu > 0 ? n_cu : 256;
-  const int64_t mt256 = (M + 255) / 256;
-  const int64_t c_short = ((int64_t)n_tiles256 * ((M + 127) / 128) + cu - 1) / cu * 84;
-  const int64_t c_tall = can_tall ? ((int64_t)n_tiles256 * mt256 + cu - 1) / cu * 122 : INT64_MAX;
-  const int64_t c_wide = can_wide ? ((int64_t)n_tiles256 * 2 * mt256 + cu - 1) / cu * 76 : INT64_MAX;
-  return c_tall <= c_wide && c_tall < c_short ? PS_TALL : (c_wide < c_short ? PS_WIDE : PS_SHORT);
+  const int nk = blocks_per_row / 4;
+  const int nu = (nk + kKSplitUnit - 1) / kKSplitUnit;
+  const int64_t mt128 = (M + 127) / 128, mt256 = (M + 255) / 256;
+  const int64_t wg_short = (int64_t)n_tiles256 * mt128;
+  // the short tile's slice count and cost
+  int ks = 1;
+  if (allow_split) {
+    if (force_ks > 0) {
+      ks = force_ks;
+    } else if (wg_short < cu) {
+      ks = (int)(cu / wg_short);
+    }
+    ks = ks > nu ? nu : ks;
+    ks = ks > kMaxKSplit ? kMaxKSplit : ks;
+    ks = ks < 1 ? 1 : ks;
+  }
+  auto short_cost = [&](int k) -> double {
+    const double steps = k == 1 ? nk : (double)kKSplitUnit * ((nu + k - 1) / k);
+    const double red = k == 1 ? 0.0 : ((double)k * M * N * 4.0 + (double)M * N * 2.0) / 3.0e6 + 2.0;
+    return (double)((wg_short * k + cu - 1) / cu) * steps * 0.84 + red;
+  };
+  // a planned (not forced) split is kept only where it is cheaper
+  if (ks > 1 && force_ks <= 0 && short_cost(ks) >= short_cost(1)) ks = 1;
+  PrefillPlan p{PS_SHORT, ks, (int)(wg_short * ks), ks == 1 ? nk : kKSplitUnit * ((nu + ks - 1) / ks)};
+  auto as_tall = [&]() { return PrefillPlan{PS_TALL, 1, (int)(n_tiles256 * mt256), nk}; };
+  auto as_wide = [&]() { return PrefillPlan{PS_WIDE, 1, (int)(n_tiles256 * 2 * mt256), nk}; };
+  if (force == PS_SHORT) return p;
+  if (force == PS_TALL) return can_tall ? as_tall() : p;
+  if (force == PS_WIDE) return can_wide ? as_wide() : p;
+  if (M <= 128) return p;
+  const double c_short = short_cost(ks);
+  const double c_tall = can_tall ? (double)((n_tiles256 * mt256 + cu - 1) / cu) * nk * 1.22 : 1e300;
+  const double c_wide = can_wide ? (double)((n_tiles256 * 2 * mt256 + cu - 1) / cu) * nk * 0.76 : 1e300;
+  if (c_tall <= c_wide && c_tall < c_short) return as_tall();
+  if (c_wide < c_short) return as_wide();
+  return p;
 }
 
 }  // namespace wal

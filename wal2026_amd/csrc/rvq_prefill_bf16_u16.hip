@@ -3,5 +3,5 @@
 
 namespace wal {
 template hipError_t prefill_entry<WAL_BF16, uint16_t>(const LayerArgs&, const DtypeArgs&, const EpilogueArgs&, int, int,
-                                              const void*, int64_t M, int shape, hipStream_t);
+                                              const void*, int64_t M, int shape, const PrefillSplit&, hipStream_t);
 }  // namespace wal

@@ -75,10 +75,19 @@ WAL_HOST_DEVICE size_t prefill_lds_bytes(int TM, int K, int rshift) {
 }
 
 
+// Split-K: ksplit > 1 workgroups share one output tile, each over a slice of
+// the k-steps (whole units of kSplitUnit steps, so that every slice starts on
+// an index group and the register slots of the unrolled producer loop keep
+// their compile-time indices), and write fp32 partial sums to part
+// [ksplit][M][out_features]; rvq_splitk_reduce_kernel sums them in slice
+// order (deterministic) and applies the epilogue.
+constexpr int kSplitUnit = 8;
+
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int TM>
 __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
                                                                       const uint16_t* __restrict__ x, int64_t M,
-                                                                      int n_mt, int rshift) {
+                                                                      int n_mt, int rshift, int ksplit,
+                                                                      float* __restrict__ part) {
   constexpr int BM = prefill_bm<TM>();
   constexpr int XP = BM * 4 / kProducerThreads;  // 16-byte x pieces per producer thread per k-step
   constexpr int BPT = PBN * 4 / kProducerThreads;  // blocks each producer thread dequantises per k-step
@@ -95,12 +104,18 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int mt = (int)(blockIdx.x % (unsigned)n_mt);
-  const int nt = (int)(blockIdx.x / (unsigned)n_mt);
+  const int rest = (int)(blockIdx.x / (unsigned)n_mt);
+  const int ks = rest % ksplit;  // k slice of this workgroup
+  const int nt = rest / ksplit;
   const FragTile<S> ti = get_frag_tile<S>(L, nt);
   const int64_t m0 = (int64_t)mt * BM;
   const int B = L.blocks_per_row;
   const int in = L.in_features;
-  const int nk = B / 4;  // B % 16 == 0 (host contract): whole k-steps, whole index groups
+  const int nk_all = B / 4;  // B % 16 == 0 (host contract): whole k-steps, whole index groups
+  // this slice's k-steps [kb, nk): the host gives every slice at least one unit
+  const int nu = (nk_all + kSplitUnit - 1) / kSplitUnit;
+  const int kb = kSplitUnit * (int)((int64_t)ks * nu / ksplit);
+  const int nk = min(nk_all, kSplitUnit * (int)((int64_t)(ks + 1) * nu / ksplit));
   const uint32_t kmax = (uint32_t)(K - 1);
 
   // Codebook table, replicated 1 << rshift times (host choice: as many
@@ -136,8 +151,8 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    __syncthreads();  // step 0 produced
-    for (int k = 0; k < nk; ++k) {
+    __syncthreads();  // step kb produced
+    for (int k = kb; k < nk; ++k) {
       const int buf = k & 1;
       u32x4_t a[TM], b[4];
 #pragma unroll
@@ -150,7 +165,25 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<XDT>(a[i], b[j], acc[i][j]);
       __syncthreads();  // buffer buf read; step k + 1 produced
     }
-    // lane holds D[m = 4q + e][n = l16] of each 16 x 16 tile
+    // lane holds D[m = 4q + e][n = l16] of each 16 x 16 tile.  (Two loops,
+    // not a branch per element: a larger unrolled body would leave acc
+    // dynamically indexed, in scratch memory.)
+    if (ksplit > 1) {
+      float* pk = part + (size_t)ks * (size_t)M * (size_t)E.ldy + ti.out_row0;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int nloc = wn * 64 + j * 16 + l16;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t m = m0 + wm * 16 * TM + i * 16 + 4 * q + e;
+            if (m < M && nloc < ti.rows) pk[m * E.ldy + nloc] = acc[i][j][e];
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -237,19 +270,21 @@ __global__ __launch_bounds__(kPrefillThreads) void rvq_prefill_kernel(LayerArgs 
 
   u32x4_t xq[4][XP];      // x pieces of steps k + 1 .. k + 4 (slot = step & 3)
   u32x4_t idq[2][S][NV];  // index bytes of two groups of 4 k-steps (slot = group & 1)
-  load_ids(0, idq[0]);
-  load_ids(1, idq[1]);
+  // (kb is a multiple of 8: the slots below are those of steps 0 .. 4 of an
+  // unsplit launch)
+  load_ids(kb / 4, idq[0]);
+  load_ids(kb / 4 + 1, idq[1]);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) load_x(j, xq[j]);
-  produce(0, 0, idq[0], xq[0]);
-  load_x(4, xq[0]);
-  __syncthreads();  // step 0 produced
+  for (int j = 0; j < 4; ++j) load_x(kb + j, xq[j]);
+  produce(kb, 0, idq[0], xq[0]);
+  load_x(kb + 4, xq[0]);
+  __syncthreads();  // step kb produced
   // Iteration k produces step k + 1 into buffer (k + 1) & 1 (read by the
   // consumers in iteration k - 1, before the previous barrier).  Unrolled by
   // 8 so that register-array indices are compile-time constants (k0 is a
   // multiple of 8): step k + 1 uses x slot (u + 1) & 3 and index slot
   // ((u + 1) >> 2) & 1; x runs four steps ahead, index bytes a group ahead.
-  for (int k0 = 0; k0 < nk; k0 += 8) {
+  for (int k0 = kb; k0 < nk; k0 += 8) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int k = k0 + u;
@@ -814,7 +849,7 @@ static hipError_t prefill_wide(const LayerArgs& L, const DtypeArgs& D, const Epi
 
 template <int S, typename IdT, int LMODE, int SEM, int XDT, int TM>
 static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
-                             int64_t M, hipStream_t st) {
+                             int64_t M, const PrefillSplit& sp, hipStream_t st) {
   // as many table copies (up to 8) as fit; the compact table is staged in
   // the W tile area first, so replication needs it to fit there
   const size_t tbl = (size_t)prefill_table_entries<S, IdT>(L.codebook_size) * lds_entry_bytes<LMODE>();
@@ -827,10 +862,13 @@ static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const Epilo
   hipError_t e = allow_max_lds(reinterpret_cast<const void*>(kern));
   if (e != hipSuccess) return e;
   const int n_mt = (int)((M + prefill_bm<TM>() - 1) / prefill_bm<TM>());
-  dim3 grid((unsigned)(L.n_tiles * (int64_t)n_mt));
+  const int ksplit = sp.part != nullptr && sp.ksplit > 1 ? sp.ksplit : 1;
+  dim3 grid((unsigned)(L.n_tiles * (int64_t)n_mt * ksplit));
   hipLaunchKernelGGL(kern, grid, dim3(kPrefillThreads), lds, st, L, D, E, reinterpret_cast<const uint16_t*>(x), M,
-                     n_mt, rshift);
-  return hipGetLastError();
+                     n_mt, rshift, ksplit, sp.part);
+  e = hipGetLastError();
+  if (e != hipSuccess || ksplit == 1) return e;
+  return launch_splitk_reduce(sp.part, ksplit, M, E, st);
 }
 
 // shape: the tile shape from plan_prefill_shape (PS_SHORT when the instance
@@ -838,24 +876,24 @@ static hipError_t prefill_tm(const LayerArgs& L, const DtypeArgs& D, const Epilo
 // rows (TM = 4, a 64 x 64 tile per wave).
 template <int S, typename IdT, int LMODE, int SEM, int XDT>
 static hipError_t prefill_go(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x,
-                             int64_t M, int shape, hipStream_t st) {
+                             int64_t M, int shape, const PrefillSplit& sp, hipStream_t st) {
   constexpr bool can_tall = tall_supported<S, IdT, LMODE>(), can_wide = wide_supported<S, IdT, LMODE>();
   if constexpr (can_tall)
     if (shape == PS_TALL) return prefill_tall<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
   if constexpr (can_wide)
     if (shape == PS_WIDE) return prefill_wide<S, IdT, LMODE, SEM, XDT>(L, D, E, x, M, st);
-  return prefill_tm<S, IdT, LMODE, SEM, XDT, 4>(L, D, E, x, M, st);
+  return prefill_tm<S, IdT, LMODE, SEM, XDT, 4>(L, D, E, x, M, sp, st);
 }
 
 template <int S, typename IdT, int XDT>
 static hipError_t prefill_sem(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                              const void* x, int64_t M, int shape, hipStream_t st) {
-  if (sem == SEM_FAST) return prefill_go<S, IdT, LM_A16, SEM_FAST, XDT>(L, D, E, x, M, shape, st);
+                              const void* x, int64_t M, int shape, const PrefillSplit& sp, hipStream_t st) {
+  if (sem == SEM_FAST) return prefill_go<S, IdT, LM_A16, SEM_FAST, XDT>(L, D, E, x, M, shape, sp, st);
   if constexpr (S == 1) {
-    return prefill_go<S, IdT, LM_A16, SEM_RECON, XDT>(L, D, E, x, M, shape, st);
+    return prefill_go<S, IdT, LM_A16, SEM_RECON, XDT>(L, D, E, x, M, shape, sp, st);
   } else {
-    if (lmode == LM_H16) return prefill_go<S, IdT, LM_H16, SEM_RECON, XDT>(L, D, E, x, M, shape, st);
-    return prefill_go<S, IdT, LM_F32, SEM_RECON, XDT>(L, D, E, x, M, shape, st);
+    if (lmode == LM_H16) return prefill_go<S, IdT, LM_H16, SEM_RECON, XDT>(L, D, E, x, M, shape, sp, st);
+    return prefill_go<S, IdT, LM_F32, SEM_RECON, XDT>(L, D, E, x, M, shape, sp, st);
   }
 }
 
@@ -863,12 +901,12 @@ static hipError_t prefill_sem(const LayerArgs& L, const DtypeArgs& D, const Epil
 // rvq_prefill_<x>_<ids>.hip.
 template <int XDT, typename IdT>
 hipError_t prefill_entry(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, int sem, int lmode,
-                         const void* x, int64_t M, int shape, hipStream_t st) {
+                         const void* x, int64_t M, int shape, const PrefillSplit& sp, hipStream_t st) {
   switch (L.num_stages) {
-    case 1: return prefill_sem<1, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, st);
-    case 2: return prefill_sem<2, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, st);
-    case 3: return prefill_sem<3, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, st);
-    default: return prefill_sem<4, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, st);
+    case 1: return prefill_sem<1, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, sp, st);
+    case 2: return prefill_sem<2, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, sp, st);
+    case 3: return prefill_sem<3, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, sp, st);
+    default: return prefill_sem<4, IdT, XDT>(L, D, E, sem, lmode, x, M, shape, sp, st);
   }
 }
 

@@ -24,28 +24,35 @@ namespace {
 
 // Cost model of the two prefill forms (microseconds), from measurements on
 // MI355X at the c4 shapes (M = 64 .. 2048, HIP events):
-//  * fused kernel: rounds of workgroups x k-steps (32 columns each) x the
-//    time of one k-step of the tile shape the library picks: 0.84 (128 x 256
-//    short), 1.22 (256 x 256 tall), 0.76 (256 x 128 wide).  Few weight-row
-//    tiles leave most CUs idle (a 4096-row layer is 16 short tiles per 128 x
+//  * fused kernel: rounds of workgroups x k-steps (32 columns each) of the
+//    largest workgroup x the time of one k-step of the tile shape the
+//    library picks: 0.84 (128 x 256 short), 1.22 (256 x 256 tall), 0.76
+//    (256 x 128 wide); with the short tile's k-steps split over several
+//    workgroups (wal_rvq_linear_ws), plus the pass that adds the fp32
+//    partials (read at 3 TB/s).  Without the split, few weight-row tiles
+//    leave most CUs idle (a 4096-row layer is 16 short tiles per 128 x
 //    rows): down_proj at M = 64 took 249 us fused, 64 us in two passes.
 //  * two passes: the dense weight written at 4.5 TB/s, then torch's GEMM,
 //    which took the weight's read at 4.0 TB/s plus its flops at 1.6 PFLOP/s
-//    (fitted over M = 64 .. 2048, within 20 %), plus 5 us of launches.  At
-//    small M the GEMM streams the weight: fused gate_up (29 MB of indices
+//    times the share of CUs its 128 x 128 output tiles fill (fitted over
+//    M = 64 .. 2048 at the c4 shapes, within 20 %), plus 5 us of launches.
+//    At small M the GEMM streams the weight: fused gate_up (29 MB of indices
 //    instead of 235 MB of weight) wins up to M = 512.
-double fused_prefill_us(const wal_rvq_layer* L, int64_t m, int tile_shape, int n_cu) {
-  const int64_t rows = tile_shape == WAL_TILE_SHORT ? 128 : 256, cols = tile_shape == WAL_TILE_WIDE ? 128 : 256;
-  const double step_us = tile_shape == WAL_TILE_TALL ? 1.22 : (tile_shape == WAL_TILE_WIDE ? 0.76 : 0.84);
-  const int64_t tiles = ((m + rows - 1) / rows) * ((L->out_features + cols - 1) / cols);
-  const int64_t rounds = (tiles + n_cu - 1) / n_cu;
-  return (double)rounds * (double)((L->in_features + 31) / 32) * step_us;
+double fused_prefill_us(const wal_rvq_layer* L, int64_t m, const wal_rvq_launch_info& info, int n_cu) {
+  const double step_us = info.tile_shape == WAL_TILE_TALL ? 1.22 : (info.tile_shape == WAL_TILE_WIDE ? 0.76 : 0.84);
+  const int64_t rounds = ((int64_t)info.grid + n_cu - 1) / n_cu;
+  double us = (double)rounds * (double)info.share * step_us;
+  if (info.k_splits > 1)
+    us += ((double)info.k_splits * m * L->out_features * 4.0 + (double)m * L->out_features * 2.0) / 3.0e6 + 2.0;
+  return us;
 }
 
-double two_pass_us(const wal_rvq_layer* L, int64_t m) {
+double two_pass_us(const wal_rvq_layer* L, int64_t m, int n_cu) {
   const double wbytes = 2.0 * (double)L->out_features * (double)L->in_features;
   const double flops = 2.0 * (double)m * (double)L->out_features * (double)L->in_features;
-  return wbytes / 4.5e6 + wbytes / 4.0e6 + flops / 1.6e9 + 5.0;
+  const double tiles = (double)((m + 127) / 128) * (double)((L->out_features + 127) / 128);
+  const double fill = tiles < n_cu ? tiles / n_cu : 1.0;
+  return wbytes / 4.5e6 + wbytes / 4.0e6 + flops / (1.6e9 * fill) + 5.0;
 }
 
 int device_cu_count() {
@@ -89,7 +96,8 @@ bool prefill_two_pass(const wal_rvq_layer* L, int64_t semantics, const void* x, 
   if (wal_rvq_linear_info(L, (int)semantics, x, m, xt, &info) != WAL_OK || info.kernel != WAL_KERNEL_PREFILL)
     return false;
   if (f != nullptr && f[0] == '1') return true;
-  return two_pass_us(L, m) < fused_prefill_us(L, m, info.tile_shape, device_cu_count());
+  const int n_cu = device_cu_count();
+  return two_pass_us(L, m, n_cu) < fused_prefill_us(L, m, info, n_cu);
 }
 
 // y[..., out_features] = x[..., in_features] W^T (+ bias) for the layer at
@@ -138,8 +146,15 @@ at::Tensor rvq_linear(const at::Tensor& x, int64_t layer, int64_t semantics, int
     at::linear_out(yv, xc.view({m, L->in_features}), w, bx);
     return y;
   }
-  const int rc = wal_rvq_linear(L, (int)semantics, (uint32_t)stage_mask, xc.data_ptr(), m, xt, b, bt, y.data_ptr(),
-                                dtype_tag(yt), st);
+  // a prefill call may split its k-steps over more workgroups: its fp32
+  // partials go to a workspace from torch's caching allocator
+  size_t ws_bytes = 0;
+  int rc = wal_rvq_linear_workspace_size(L, (int)semantics, xc.data_ptr(), m, xt, &ws_bytes);
+  TORCH_CHECK(rc == WAL_OK, "wal2026_amd error ", rc, ": ", wal_last_error());
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte));
+  rc = wal_rvq_linear_ws(L, (int)semantics, (uint32_t)stage_mask, xc.data_ptr(), m, xt, b, bt, y.data_ptr(),
+                         dtype_tag(yt), ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, st);
   TORCH_CHECK(rc == WAL_OK, "wal2026_amd error ", rc, ": ", wal_last_error());
   return y;
 }

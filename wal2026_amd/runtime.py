@@ -248,7 +248,8 @@ def _launch_info(layer: "_lib.WalLayer", semantics: int, x: Tensor) -> dict:
         out.update(x_mode=_lib.XMODE_NAMES[info.x_mode], table_slots=info.table_slots, grid=info.grid,
                    share=info.share, lds_bytes=info.lds_bytes)
     elif info.kernel == _lib.KERNEL_PREFILL:
-        out["tile_shape"] = _TILE_NAMES[info.tile_shape]
+        out.update(tile_shape=_TILE_NAMES[info.tile_shape], grid=info.grid, k_steps=info.share,
+                   k_splits=info.k_splits)
         # the torch operator's choice for an output in x's dtype: the dense
         # weight (wal_rvq_reconstruct) then torch's GEMM, or the fused kernel
         out["two_pass"] = bool(_lib.ops().rvq_prefill_two_pass(ctypes.addressof(layer), semantics,
