@@ -191,6 +191,20 @@ int wal_rvq_linear_ws(const wal_rvq_layer* layer, int semantics,
                       int y_dtype, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* wal_rvq_linear_ws for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * the split-K partials go to a scratch array the library holds in device
+ * memory, 64 MiB per GPU (kept until the process ends; its device address is
+ * looked up once per device on the first call that needs it).  A call whose
+ * partials would exceed 64 MiB (wal_rvq_linear_workspace_size) returns
+ * WAL_ESIZE.  Calls that overlap on one GPU share the array and race: issue
+ * them on one stream.  No counterpart in the reference: an entry point for
+ * callers that cannot allocate. */
+int wal_rvq_linear_noalloc(const wal_rvq_layer* layer, int semantics,
+                           uint32_t active_stage_mask, const void* x, int64_t m,
+                           int x_dtype, const void* bias, int bias_dtype, void* y,
+                           int y_dtype, void* stream);
+
 /* Bytes of workspace wal_rvq_linear_ws uses for these arguments (0: no split;
  * x is only checked for alignment).  No reference counterpart. */
 int wal_rvq_linear_workspace_size(const wal_rvq_layer* layer, int semantics, const void* x,

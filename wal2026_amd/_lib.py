@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "wal_rvq_reconstruct",
     "wal_rvq_linear",
     "wal_rvq_linear_ws",
+    "wal_rvq_linear_noalloc",
     "wal_rvq_linear_workspace_size",
     "wal_rvq_linear_info",
     "wal_rvq_group_linear_matmul",
@@ -147,6 +148,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wal_rvq_linear.argtypes = [ctypes.POINTER(WalLayer), i32, u32, vp, i64, i32, vp, i32, vp, i32, vp]
     L.wal_rvq_linear_ws.restype = i32
     L.wal_rvq_linear_ws.argtypes = [ctypes.POINTER(WalLayer), i32, u32, vp, i64, i32, vp, i32, vp, i32, vp, sz, vp]
+    L.wal_rvq_linear_noalloc.restype = i32
+    L.wal_rvq_linear_noalloc.argtypes = [ctypes.POINTER(WalLayer), i32, u32, vp, i64, i32, vp, i32, vp, i32, vp]
     L.wal_rvq_linear_workspace_size.restype = i32
     L.wal_rvq_linear_workspace_size.argtypes = [ctypes.POINTER(WalLayer), i32, vp, i64, i32, ctypes.POINTER(sz)]
     L.wal_rvq_linear_info.restype = i32

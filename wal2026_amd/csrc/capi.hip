@@ -33,6 +33,45 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(WAL_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// ---- scratch of wal_rvq_linear_noalloc ---------------------------------------
+// The split-K partials of the entry point that allocates nothing live in this
+// file-scope device array: every GPU the library runs on holds its own copy
+// until the process ends.  In host code `scratch` names a host-side stand-in,
+// not a device address: the device address is taken once per device with
+// hipGetSymbolAddress (that device current) and only that pointer is passed
+// to kernels.  Calls that overlap on one GPU share the array and race.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch` (set up on the first call on a
+// device), or nullptr with the error recorded.
+void* scratch_for_current_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(WAL_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(WAL_EUNSUPPORTED, "device %d: the scratch table holds %d devices", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      fail(WAL_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
 bool is_float_dtype(int dt) { return dt == WAL_F16 || dt == WAL_BF16 || dt == WAL_F32; }
 bool is_half_dtype(int dt) { return dt == WAL_F16 || dt == WAL_BF16; }
 bool is_id_dtype(int dt) { return dt == WAL_U8 || dt == WAL_I16 || dt == WAL_U16 || dt == WAL_I32; }
@@ -502,6 +541,24 @@ int wal_rvq_linear_ws(const wal_rvq_layer* layer, int semantics, uint32_t active
                       void* workspace, size_t workspace_bytes, void* stream) {
   return linear_impl(layer, semantics, active_stage_mask, x, m, x_dtype, bias, bias_dtype, y, y_dtype, workspace,
                      workspace_bytes, stream);
+}
+
+int wal_rvq_linear_noalloc(const wal_rvq_layer* layer, int semantics, uint32_t active_stage_mask, const void* x,
+                           int64_t m, int x_dtype, const void* bias, int bias_dtype, void* y, int y_dtype,
+                           void* stream) {
+  g_err[0] = 0;
+  size_t need = 0;
+  int rc = wal_rvq_linear_workspace_size(layer, semantics, x, m, x_dtype, &need);
+  if (rc) return rc;
+  if (need > kNoAllocScratchBytes)
+    return fail(WAL_ESIZE, "this call needs %zu bytes of split-K scratch, the maximum is %zu (use wal_rvq_linear_ws)",
+                need, kNoAllocScratchBytes);
+  void* ptr = nullptr;
+  if (need > 0 && (ptr = scratch_for_current_device()) == nullptr) return WAL_EHIP;
+  // every partial the kernels read is written first in the same call: nothing
+  // in the scratch has to start at zero
+  return linear_impl(layer, semantics, active_stage_mask, x, m, x_dtype, bias, bias_dtype, y, y_dtype, ptr,
+                     need > 0 ? kNoAllocScratchBytes : 0, stream);
 }
 
 int wal_rvq_linear_workspace_size(const wal_rvq_layer* layer, int semantics, const void* x, int64_t m, int x_dtype,
