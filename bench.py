@@ -343,17 +343,22 @@ def pmc_path(kind: str, config: str, name: str, two_pass: bool = False) -> str:
 
 def roofline_of(st: Stack, name: str, nbytes: int, us: float, pmc_summary: str | None) -> dict:
     cfg = st.cfg
+    # the committed counter summaries are for each config's own M
+    own_m = cfg.m == synth.CONFIGS[cfg.name].m
     if cfg.m > 16:
         flops = st.launch_flops(name)
         tflops = flops / (us * 1e-6) / 1e12
         x = st.xs[next(k for n, k, _ in st.fused_launches() if n == name)]
-        two_pass = st.stack[0][name].launch_info(x).get("two_pass", False)
+        info = st.stack[0][name].launch_info(x)
+        two_pass = info.get("two_pass", False)
         if two_pass:
             kernel = (f"{name} launch, two passes: rvq_dequant8_kernel (the dense weight, bit-exact) + torch's "
                       f"bf16 GEMM (hipBLASLt), {flops} flop")
-            pmc_summary = pmc_path("prefill", cfg.name, name, two_pass=True)
+            pmc_summary = pmc_path("prefill", cfg.name, name, two_pass=True) if own_m else None
         else:
-            kernel = f"rvq_prefill_*_kernel, launcher's choice ({name}, {flops} flop)"
+            kernel = (f"rvq_prefill_*_kernel, {info['tile_shape']} tile, {info['k_splits']} k slice(s) "
+                      f"({name}, {flops} flop)")
+            pmc_summary = pmc_summary if own_m else None
         out = {"bound": "mfma", "kernel": kernel, "two_pass": two_pass,
                "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "avg_launch_us": round(us, 3),
@@ -365,7 +370,7 @@ def roofline_of(st: Stack, name: str, nbytes: int, us: float, pmc_summary: str |
             out["fused_kernel"] = {"kernel": f"rvq_prefill_*_kernel, launcher's choice ({name})",
                                    "avg_launch_us": round(fus, 3), "achieved": round(ftf, 1),
                                    "frac": round(ftf / BF16_PEAK_TFLOPS, 4),
-                                   "traffic": traffic_bytes(pmc_path("prefill", cfg.name, name))}
+                                   "traffic": traffic_bytes(pmc_path("prefill", cfg.name, name)) if own_m else None}
         return out
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"bound": "hbm", "kernel": f"rvq_decode_kernel ({name}, {nbytes} compressed bytes)",
@@ -374,10 +379,14 @@ def roofline_of(st: Stack, name: str, nbytes: int, us: float, pmc_summary: str |
             "traffic": traffic_bytes(pmc_summary) if pmc_summary else None}
 
 
-def secondary(name: str, layers: int | None, steps: int, warmup: int, dev: torch.device) -> dict:
-    """One line for another config: fused-step tokens/s over a graph-captured
-    stack and the dominant launch against its roofline (HIP events)."""
+def secondary(name: str, layers: int | None, steps: int, warmup: int, dev: torch.device,
+              m: int | None = None) -> dict:
+    """One line for another config (optionally at another M): fused-step
+    tokens/s over a graph-captured stack and the dominant launch against its
+    roofline (HIP events)."""
     cfg = synth.CONFIGS[name]
+    if m is not None and m != cfg.m:
+        cfg = synth.Config(**{**cfg.__dict__, "m": m})
     layers = layers or cfg.layers
     log(f"secondary {name}: building {layers} layers")
     st = Stack(cfg, layers, dev)
@@ -390,7 +399,8 @@ def secondary(name: str, layers: int | None, steps: int, warmup: int, dev: torch
                        f"{str(cfg.ids_dtype()).replace('torch.', '')} ids, {layers} of {cfg.layers} layers timed, "
                        f"fused, one HIP graph per step, {steps} steps; tok/s over all {cfg.layers} layers",
            "tok_s": round(cfg.m * 1e6 / (us_layer * cfg.layers), 2), "us_per_layer": round(us_layer, 3),
-           "roofline": roofline_of(st, dom_name, dom_bytes, us, pmc_path(kind, name, dom_name))}
+           "roofline": roofline_of(st, dom_name, dom_bytes, us,
+                                   pmc_path(kind, name, dom_name) if m is None else None)}
     if kind == "decode":
         out["step_hbm_fraction"] = round(cfg.compressed_bytes_per_layer() * layers / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                          4)
@@ -640,6 +650,9 @@ def main() -> int:
         result["config"]["secondary"] = {
             "c5": secondary("c5", None, 128, args.warmup, dev),
             "c4": secondary("c4", 4, 10, 2, dev),
+            # a batch of 256 prefill rows: the operator picks per launch
+            # between the split-K fused kernel and the two passes
+            "c4_m256": secondary("c4", 4, 10, 2, dev, m=256),
         }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
