@@ -72,6 +72,14 @@ def test_forward_on_cpu_fails_loudly():
     route = w.PackedIDRouteLinear(torch.zeros(4, 8, dtype=torch.int32), torch.ones(3, 2), torch.ones(4, 1))
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         route(torch.zeros(1, 8))
+    # the operators refuse CPU tensors too (no CPU compute path)
+    from wal2026_amd import _lib
+    ops = _lib.ops()
+    xc = torch.zeros(1, 32, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ops.rvq_linear(xc, 1, 0, 0, None, None)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ops.rvq_linear_out(xc, 1, 0, 0, None, torch.empty(1, 16, dtype=torch.bfloat16))
 
 
 def test_unported_strategies_raise():

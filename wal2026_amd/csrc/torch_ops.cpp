@@ -100,27 +100,27 @@ bool prefill_two_pass(const wal_rvq_layer* L, int64_t semantics, const void* x, 
   return two_pass_us(L, m, n_cu) < fused_prefill_us(L, m, info, n_cu);
 }
 
-// y[..., out_features] = x[..., in_features] W^T (+ bias) for the layer at
-// address `layer` (a wal_rvq_layer*): wal_rvq_linear on the current stream,
-// or for a large prefill the dense weight and torch's GEMM (prefill_two_pass).
-at::Tensor rvq_linear(const at::Tensor& x, int64_t layer, int64_t semantics, int64_t stage_mask,
-                      const c10::optional<at::Tensor>& bias, c10::optional<at::ScalarType> out_dtype) {
+const wal_rvq_layer* checked_layer(const at::Tensor& x, int64_t layer) {
   const wal_rvq_layer* L = reinterpret_cast<const wal_rvq_layer*>(layer);
   TORCH_CHECK(L != nullptr, "wal2026_amd: null layer descriptor");
   TORCH_CHECK(x.is_cuda(), "wal2026_amd: x must be on a ROCm device (got ", x.device(), ")");
   TORCH_CHECK(x.dim() >= 1 && x.size(-1) == L->in_features, "wal2026_amd: x has ", x.size(-1),
               " features, the layer ", L->in_features);
+  TORCH_CHECK(dtype_tag(x.scalar_type()) >= 0, "wal2026_amd: unsupported activation dtype ", x.scalar_type());
+  return L;
+}
+
+// y[..., out_features] = x[..., in_features] W^T (+ bias) into y (contiguous,
+// on x's device): wal_rvq_linear_ws on the current stream, or the dense weight
+// and torch's GEMM where that form is faster (prefill_two_pass).
+void linear_into(const wal_rvq_layer* L, const at::Tensor& x, int64_t semantics, int64_t stage_mask,
+                 const c10::optional<at::Tensor>& bias, at::Tensor& y) {
   const int xt = dtype_tag(x.scalar_type());
-  TORCH_CHECK(xt >= 0, "wal2026_amd: unsupported activation dtype ", x.scalar_type());
+  const at::ScalarType yt = y.scalar_type();
   at::Tensor xc = x.contiguous();
   if (reinterpret_cast<uintptr_t>(xc.data_ptr()) % 16 != 0) xc = xc.clone();  // the fused kernels load 16 B
-  const at::ScalarType yt = out_dtype.has_value() ? *out_dtype : x.scalar_type();
-  TORCH_CHECK(dtype_tag(yt) >= 0, "wal2026_amd: unsupported output dtype ", yt);
-  std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end());
-  shape.back() = L->out_features;
-  at::Tensor y = at::empty(shape, x.options().dtype(yt));
   const int64_t m = x.numel() / L->in_features;
-  if (m == 0) return y;
+  if (m == 0) return;
   const void* b = nullptr;
   int bt = WAL_F32;
   at::Tensor bc;
@@ -144,7 +144,7 @@ at::Tensor rvq_linear(const at::Tensor& x, int64_t layer, int64_t semantics, int
     if (bc.defined()) bx = bc.to(x.scalar_type());
     at::Tensor yv = y.view({m, L->out_features});
     at::linear_out(yv, xc.view({m, L->in_features}), w, bx);
-    return y;
+    return;
   }
   // a prefill call may split its k-steps over more workgroups: its fp32
   // partials go to a workspace from torch's caching allocator
@@ -156,7 +156,36 @@ at::Tensor rvq_linear(const at::Tensor& x, int64_t layer, int64_t semantics, int
   rc = wal_rvq_linear_ws(L, (int)semantics, (uint32_t)stage_mask, xc.data_ptr(), m, xt, b, bt, y.data_ptr(),
                          dtype_tag(yt), ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, st);
   TORCH_CHECK(rc == WAL_OK, "wal2026_amd error ", rc, ": ", wal_last_error());
+}
+
+// The module forward's op: y allocated with torch's caching allocator, in
+// out_dtype (default x's dtype).
+at::Tensor rvq_linear(const at::Tensor& x, int64_t layer, int64_t semantics, int64_t stage_mask,
+                      const c10::optional<at::Tensor>& bias, c10::optional<at::ScalarType> out_dtype) {
+  const wal_rvq_layer* L = checked_layer(x, layer);
+  const at::ScalarType yt = out_dtype.has_value() ? *out_dtype : x.scalar_type();
+  TORCH_CHECK(dtype_tag(yt) >= 0, "wal2026_amd: unsupported output dtype ", yt);
+  std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end());
+  shape.back() = L->out_features;
+  at::Tensor y = at::empty(shape, x.options().dtype(yt));
+  linear_into(L, x, semantics, stage_mask, bias, y);
   return y;
+}
+
+// The same into a caller's output (its dtype is the output dtype): for code
+// that keeps its buffers across calls, such as a captured HIP graph.
+at::Tensor& rvq_linear_out(const at::Tensor& x, int64_t layer, int64_t semantics, int64_t stage_mask,
+                           const c10::optional<at::Tensor>& bias, at::Tensor& out) {
+  const wal_rvq_layer* L = checked_layer(x, layer);
+  TORCH_CHECK(out.is_cuda() && out.device() == x.device(), "wal2026_amd: out must be on the device of x");
+  TORCH_CHECK(out.is_contiguous(), "wal2026_amd: out must be contiguous");
+  TORCH_CHECK(dtype_tag(out.scalar_type()) >= 0, "wal2026_amd: unsupported output dtype ", out.scalar_type());
+  std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end());
+  shape.back() = L->out_features;
+  TORCH_CHECK(out.sizes().vec() == shape, "wal2026_amd: out has shape ", out.sizes(), ", the call needs ",
+              at::IntArrayRef(shape));
+  linear_into(L, x, semantics, stage_mask, bias, out);
+  return out;
 }
 
 // Whether rvq_linear takes the two-pass form for m activation rows of dtype
@@ -175,13 +204,26 @@ at::Tensor rvq_linear_cpu(const at::Tensor& x, int64_t, int64_t, int64_t, const 
   TORCH_CHECK(false, "wal2026_amd: x must be on a ROCm device (got ", x.device(),
               "); the HIP library is the only compute path");
 }
+at::Tensor& rvq_linear_out_cpu(const at::Tensor& x, int64_t, int64_t, int64_t, const c10::optional<at::Tensor>&,
+                               at::Tensor& out) {
+  TORCH_CHECK(false, "wal2026_amd: x must be on a ROCm device (got ", x.device(),
+              "); the HIP library is the only compute path");
+  return out;
+}
 
 }  // namespace
 
 TORCH_LIBRARY(wal2026_amd, m) {
   m.def("rvq_linear(Tensor x, int layer, int semantics, int stage_mask, Tensor? bias, ScalarType? out_dtype) -> Tensor");
+  m.def("rvq_linear_out(Tensor x, int layer, int semantics, int stage_mask, Tensor? bias, Tensor(a!) out) -> Tensor(a!)");
   m.def("rvq_prefill_two_pass(int layer, int semantics, int m, ScalarType dtype) -> bool", &rvq_prefill_two_pass);
 }
 
-TORCH_LIBRARY_IMPL(wal2026_amd, CUDA, m) { m.impl("rvq_linear", rvq_linear); }
-TORCH_LIBRARY_IMPL(wal2026_amd, CPU, m) { m.impl("rvq_linear", rvq_linear_cpu); }
+TORCH_LIBRARY_IMPL(wal2026_amd, CUDA, m) {
+  m.impl("rvq_linear", rvq_linear);
+  m.impl("rvq_linear_out", rvq_linear_out);
+}
+TORCH_LIBRARY_IMPL(wal2026_amd, CPU, m) {
+  m.impl("rvq_linear", rvq_linear_cpu);
+  m.impl("rvq_linear_out", rvq_linear_out_cpu);
+}
