@@ -256,7 +256,7 @@ struct Route {
 int route_linear(const wal_rvq_layer& L, int sem, int x_dtype, const void* x, int64_t m, bool allow_split, Route* r) {
   r->kernel = WAL_KERNEL_GENERIC;
   r->shape = -1;
-  r->dp = DecodePlan{-1, -1, -1, -1, 0};
+  r->dp = DecodePlan{-1, -1, -1, -1, 0, 1};
   r->pp = PrefillPlan{-1, 1, -1, -1};
   if (m == 0) {
     r->kernel = WAL_KERNEL_NONE;

@@ -186,11 +186,12 @@ WAL_DEVICE void stage_table(uint32_t dst_off, const uint8_t* img, const GroupPtr
   else stage_codebooks<S, LMODE, SEM, XDT, SCALE_TABLE>(dst, p, K, D, rs);
 }
 
-template <int S, typename IdT, int LMODE, int SEM, int XDT, int XMODE, bool SCALED>
+template <int S, typename IdT, int LMODE, int SEM, int XDT, int XMODE, bool SCALED, int G>
 __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs L, DtypeArgs D, EpilogueArgs E,
                                                                        const uint16_t* __restrict__ x, int M,
                                                                        int max_tiles, int nslots) {
   static_assert(!SCALED || LMODE == LM_A16, "scaled tables hold one 16-bit value per element");
+  static_assert(G == 1 || XMODE == XM_REG, "wave groups: one chunk per wave, x fragments in registers");
   // Touch every cache line of the kernel arguments at once: otherwise the
   // compiler loads each field where it is first used, and every first touch
   // of a line is its own dependent scalar-memory round trip.
@@ -221,7 +222,16 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   const int nl = lane & 15;
   const int q = lane >> 4;
   const int nchunk = (B + 63) >> 6;
-  const int CPT = (nchunk + NW - 1) / NW;
+  // G wave groups (G > 1 when a row has at most NW / G chunks): group g =
+  // wave / NWG computes the range's tiles j with j % G == g, wave w taking
+  // chunk w % NWG of them, so no wave idles for want of a chunk.  Every wave
+  // still walks every tile (table slots, restages and partial parking stay
+  // in lockstep); a wave's partial for a tile it does not compute is the
+  // zero it started the tile with, so the sums are those of G == 1.
+  constexpr int NWG = NW / G;
+  const int wch = G == 1 ? wave : wave % NWG;  // this wave's chunk (first of CPT)
+  const int wgr = G == 1 ? 0 : wave / NWG;    // this wave's group
+  const int CPT = (nchunk + NWG - 1) / NWG;
   // tiles [t_begin, t_begin + n_tiles_wg): T split as evenly as possible
   const int T = L.n_tiles;
   const int tq = T / (int)gridDim.x, tr = T % (int)gridDim.x, bx = blockIdx.x;
@@ -326,8 +336,8 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
     // the range, or a chunk past the row, gets an out-of-range offset and
     // reads zeros without touching memory.  Rows past the tile re-read its
     // last row (outputs of those rows are never stored).
-    const int c = wave + NW * is_c;
-    const bool ok = is_t < n_tiles_wg && c < nchunk;  // uniform
+    const int c = wch + NWG * is_c;
+    const bool ok = is_t < n_tiles_wg && c < nchunk && (G == 1 || is_t % G == wgr);  // uniform
     const int base = min(c * 64 + 16 * q, B - 16);
     const int r = iti.row0 + min(nl, tile_rows<S>(iti) - 1);
     const uint32_t off = ok ? (uint32_t)((r * B + base) * (int)sizeof(IdT)) : kBufOOB;
@@ -397,7 +407,7 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
   __syncthreads();
 
   if constexpr (XMODE == XM_REG) {
-    const int base = wave * 64 + 16 * q;
+    const int base = wch * 64 + 16 * q;
     const uint8_t* xp = base < B ? reinterpret_cast<const uint8_t*>(xs + (size_t)xm * in + (size_t)base * 8) : zrow;
 #pragma unroll
     for (int tt = 0; tt < 16; ++tt) xreg[tt] = *reinterpret_cast<const u32x4_t*>(xp + tt * 16);
@@ -456,8 +466,8 @@ __global__ __launch_bounds__(kDecodeMaxThreads) void rvq_decode_kernel(LayerArgs
 #pragma unroll
         for (int v = 0; v < NV; ++v) cur[s][v] = ring[j][s][v];
       if (i0 + j + PF < n_items) issue(j);
-      const int c = wave + NW * ct_c;
-      if (live && c < nchunk) {  // uniform across the wave
+      const int c = wch + NWG * ct_c;
+      if (live && c < nchunk && (G == 1 || ct_t % G == wgr)) {  // uniform across the wave
         const int base = c * 64 + 16 * q;
         const bool seg_ok = base < B;  // lanes past the row read zero activations
         // lanes past the row read the 256-byte zero row instead
@@ -614,11 +624,14 @@ template <int S, typename IdT, int LMODE, int SEM, int XDT, bool SCALED>
 static hipError_t decode_go(const LayerArgs& L, const DtypeArgs& D, const EpilogueArgs& E, const void* x, int M,
                             const DecodePlan& P, hipStream_t st) {
   if (P.grid < 1) return hipSuccess;
-  auto kern = P.xmode == XM_REG    ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_REG, SCALED>
-              : P.xmode == XM_LDS  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_LDS, SCALED>
-              : P.xmode == XM_GREG ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GREG, SCALED>
-              : P.xmode == XM_GTR  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GTR, SCALED>
-                                   : rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GLOBAL, SCALED>;
+  auto kern = P.xmode == XM_REG    ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_REG, SCALED, 1>
+              : P.xmode == XM_LDS  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_LDS, SCALED, 1>
+              : P.xmode == XM_GREG ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GREG, SCALED, 1>
+              : P.xmode == XM_GTR  ? rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GTR, SCALED, 1>
+                                   : rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_GLOBAL, SCALED, 1>;
+  if constexpr (!SCALED) {
+    if (P.xmode == XM_REG && P.groups == 2) kern = rvq_decode_kernel<S, IdT, LMODE, SEM, XDT, XM_REG, false, 2>;
+  }
   hipError_t e = allow_max_lds(reinterpret_cast<const void*>(kern));
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(P.grid), dim3(kDecodeMaxThreads), P.lds, st, L, D, E,

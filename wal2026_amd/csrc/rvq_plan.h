@@ -56,6 +56,7 @@ struct DecodePlan {
   int grid;
   int share;  // tiles of the largest workgroup share
   size_t lds;
+  int groups;  // wave groups (2: two halves of the waves take alternate tiles)
 };
 
 // WAL2026_DECODE_XMODE, or -1 (planner's choice); -2 for an unknown value.
@@ -126,6 +127,10 @@ inline bool plan_decode(int esz, int S, int K, int M, int in, int B, int n_tiles
       out->grid = g;
       out->share = (n_tiles + g - 1) / g;
       out->lds = decode_lds_bytes(esz, S, K, xlds, M, in, nw, out->share, c.nslots, xscr);
+      // x in registers with at most half as many chunks per row as waves
+      // (in_features <= 2048): two wave groups on alternate tiles, when a
+      // workgroup holds more than one tile
+      out->groups = c.xmode == XM_REG && 2 * nchunk <= nw && out->share > 1 ? 2 : 1;
       found = true;
     }
     if (rounds <= 1) break;
