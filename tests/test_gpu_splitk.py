@@ -145,3 +145,14 @@ def test_module_forward_passes_a_workspace(gpu_device, clean_env):
     assert rel_err(y, c_oracle.linear_f64(x.cpu(), w)) <= 4e-3
     # the same bits as the C ABI's split launch
     assert torch.equal(y.view(torch.int16), _call(mod, x, torch.bfloat16).view(torch.int16))
+
+
+def test_split_k_fp16_activations(gpu_device, clean_env):
+    """fp16 x (the weight rounded to fp16, fp16 MFMAs) through 16 slices."""
+    mod, _ = _module("s2_u8_m64", gpu_device)
+    x = torch.randn(64, 4096, generator=torch.Generator().manual_seed(12)).to(torch.float16).to(gpu_device)
+    assert mod.launch_info(x)["k_splits"] == 16
+    y = _call(mod, x, torch.float32)
+    w = oracle_weight(module_buffers_as_encoding(mod), torch.float16)
+    assert rel_err(y, c_oracle.linear_f64(x.cpu(), w)) <= 2e-3
+    assert rel_err(y, _call(mod, x, torch.float32, split=False)) <= 1e-5
