@@ -41,7 +41,8 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from wal2026_amd import FusedBlockRVQLinears, PackedGroupedBlockRVQLinear, _lib, synth  # noqa: E402
+from wal2026_amd import (FusedBlockRVQLinears, PackedGroupedBlockRVQLinear, _lib, fuse_sibling_linears,  # noqa: E402
+                         synth, unfuse_sibling_linears)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 # linears of a layer that read the same activation, fused into one launch
@@ -585,6 +586,15 @@ def main() -> int:
     ms_unfused = st.graph_ms(st.step_unfused, args.steps, args.warmup)
     log(f"timing {args.steps} eager drop-in steps (no graph)")
     ms_eager, ms_eager_host = st.eager_ms(st.step_unfused, args.steps, args.warmup)
+    # the drop-in step again with each layer's q/k/v and gate/up linked by
+    # fuse_sibling_linears: the model's unchanged calls, the fused launches
+    log("timing the drop-in step with fuse_sibling_linears (graph, then eager)")
+    for layer in st.stack:
+        fuse_sibling_linears(torch.nn.ModuleDict({n: layer[n] for n, _, _ in cfg.shapes()}))
+    ms_sib = st.graph_ms(st.step_unfused, args.steps, args.warmup)
+    ms_sib_eager, _ = st.eager_ms(st.step_unfused, args.steps, args.warmup)
+    for layer in st.stack:
+        unfuse_sibling_linears(torch.nn.ModuleDict({n: layer[n] for n, _, _ in cfg.shapes()}))
     log(f"timing {args.steps} graph replays of the fused step ({len(st.fused_launches())} launches per layer)")
     ms_per_step = st.graph_ms(st.step_fused, args.steps, args.warmup)
     tok_s = cfg.m * 1000.0 / ms_per_step
@@ -635,6 +645,8 @@ def main() -> int:
             "unfused_tok_s": round(cfg.m * 1000.0 / ms_unfused, 3),
             "unfused_us_per_layer": round(ms_unfused * 1000.0 / layers, 3),
             "eager_unfused_tok_s": round(cfg.m * 1000.0 / ms_eager, 3),
+            "dropin_sibling_fused_tok_s": round(cfg.m * 1000.0 / ms_sib, 3),
+            "eager_dropin_sibling_fused_tok_s": round(cfg.m * 1000.0 / ms_sib_eager, 3),
             "eager_us_per_forward": round(ms_eager * 1000.0 / n_linears, 3),
             "eager_host_issue_us_per_forward": round(ms_eager_host * 1000.0 / n_linears, 3),
             "per_launch": per_launch,

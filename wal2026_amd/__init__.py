@@ -26,11 +26,13 @@ from .runtime import (
     PackedBlockRVQGroup,
     PackedGroupedBlockRVQLinear,
     PackedIDRouteLinear,
+    fuse_sibling_linears,
     replace_with_packed_block_rvq,
     replace_with_preencoded_packed_block_rvq,
     set_effective_stages_by_name,
     set_effective_stages_from_map,
     set_global_effective_stages,
+    unfuse_sibling_linears,
 )
 
 __all__ = [
@@ -47,6 +49,7 @@ __all__ = [
     "dense_bf16_storage_bytes",
     "encode_block_residual_vq",
     "encode_grouped_block_residual_vq",
+    "fuse_sibling_linears",
     "id_route_linear_matmul",
     "ideal_id_bits_per_weight",
     "load_grouped_encoding_map",
@@ -58,4 +61,5 @@ __all__ = [
     "set_effective_stages_from_map",
     "set_global_effective_stages",
     "storage_megabytes",
+    "unfuse_sibling_linears",
 ]

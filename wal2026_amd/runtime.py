@@ -495,6 +495,7 @@ class PackedGroupedBlockRVQLinear(nn.Module):
         self._desc: _LayerDesc | None = None
         # (device, x dtype, fast) -> (layer address, semantics, stage mask, stage epoch, layer struct)
         self._calls: dict = {}
+        self._sibling: _SiblingFusion | None = None  # fuse_sibling_linears
         prev = 0
         for r0, r1 in self.row_slices:
             if r0 != prev or r1 <= r0:
@@ -628,6 +629,8 @@ class PackedGroupedBlockRVQLinear(nn.Module):
         return torch.cat(parts, dim=-1)
 
     def forward(self, x: Tensor) -> Tensor:
+        if self._sibling is not None:
+            return self._sibling.output(self, x)
         s = self.matmul_strategy
         if s in _RECON_STRATEGIES:
             return self._hip_linear(x, fast=False)
@@ -744,6 +747,86 @@ class FusedBlockRVQLinears(nn.Module):
             outs.append(y[..., o0:o0 + n])
             o0 += n
         return tuple(outs)
+
+
+class _SiblingFusion:
+    """The fused launch behind linears linked by fuse_sibling_linears.
+
+    The first of them called on an input x runs ONE FusedBlockRVQLinears
+    launch for all and returns its own output; the others, called next on the
+    same tensor (same object, unchanged since: its version counter, and the
+    same stage caps), return theirs from that launch instead of launching
+    again.  A call on any other input launches afresh.  Each output is what
+    the linear's own forward returns, bit for bit (the same per-row
+    arithmetic); for several rows of x they are column slices of one buffer,
+    as torch.split returns them.
+    """
+
+    def __init__(self, linears) -> None:
+        self.fused = FusedBlockRVQLinears(linears)
+        self.ids = [id(lin) for lin in linears]
+        self._x: Tensor | None = None
+        self._key: tuple | None = None
+        self._outs: tuple | None = None
+        self._pending: set[int] = set()
+
+    def output(self, lin: "PackedGroupedBlockRVQLinear", x: Tensor) -> Tensor:
+        i = self.ids.index(id(lin))
+        try:
+            ver = x._version
+        except RuntimeError:  # inference-mode tensors keep no version counter
+            ver = None
+        key = (ver, _STAGE_EPOCH[0])
+        if self._outs is not None and x is self._x and key == self._key and i in self._pending:
+            self._pending.discard(i)
+            out = self._outs[i]
+            if not self._pending:
+                self._x = self._outs = None
+            return out
+        outs = self.fused(x)
+        self._x, self._key, self._outs = x, key, outs
+        self._pending = set(range(len(self.ids))) - {i}
+        return outs[i]
+
+
+# Linears that read the same input in the reference's decoder layers
+# (TARGET_LINEAR_SUFFIXES, src/runtime.py:41-49).
+SIBLING_GROUPS = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"))
+
+
+def fuse_sibling_linears(model: nn.Module, groups=SIBLING_GROUPS) -> list[str]:
+    """Link the PackedGroupedBlockRVQLinear children of each module that
+    holds a whole sibling group (q/k/v, gate/up) so that the model's unchanged
+    forward runs each group as one launch (_SiblingFusion): the import swap
+    then gets the fused launches without changes to the model code.  Groups
+    whose linears cannot share a launch (different in_features, or RECON
+    beside FAST strategies) are left alone.  Returns the linked groups'
+    names.  No reference counterpart (the reference launches each linear,
+    src/runtime.py:1362); unlink with unfuse_sibling_linears."""
+    linked = []
+    for name, parent in model.named_modules():
+        for members in groups:
+            lins = [getattr(parent, m, None) for m in members]
+            if not all(isinstance(lin, PackedGroupedBlockRVQLinear) for lin in lins):
+                continue
+            try:
+                fusion = _SiblingFusion(lins)
+            except (TypeError, ValueError):
+                continue
+            for lin in lins:
+                lin._sibling = fusion
+            linked.append(f"{name}.{{{','.join(members)}}}" if name else "{" + ",".join(members) + "}")
+    return linked
+
+
+def unfuse_sibling_linears(model: nn.Module) -> int:
+    """Undo fuse_sibling_linears; returns the number of linears unlinked."""
+    n = 0
+    for mod in model.modules():
+        if isinstance(mod, PackedGroupedBlockRVQLinear) and mod._sibling is not None:
+            mod._sibling = None
+            n += 1
+    return n
 
 
 class _GroupView:
