@@ -105,6 +105,12 @@ def test_full_prefill_fused_gate_up(gpu_device, monkeypatch):
     from wal2026_amd import FusedBlockRVQLinears
 
     monkeypatch.delenv("WAL2026_PREFILL_TILE", raising=False)
+    # the fused kernel, unsplit, for the module forwards too: its per-row
+    # arithmetic is the same in the fused and the separate launches, so they
+    # agree bit for bit (the two-pass form's library GEMM may sum a 28672-row
+    # and a 14336-row product in different orders)
+    monkeypatch.setenv("WAL2026_PREFILL_TWO_PASS", "0")
+    monkeypatch.setenv("WAL2026_PREFILL_KSPLIT", "1")
     print("[fullsize] prefill c4 gate_up 2048x28672x4096", flush=True)
     cfg, gate, gen = _layer("c4", 14336, 4096, gpu_device, seed=0)
     _, up, _ = _layer("c4", 14336, 4096, gpu_device, seed=1)

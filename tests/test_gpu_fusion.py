@@ -40,7 +40,11 @@ def _linears(spec, device, bias: bool):
 @pytest.mark.parametrize("spec", FUSIONS, ids=[f[0] for f in FUSIONS])
 @pytest.mark.parametrize("m", [1, 4, 16, 40])
 @pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float16], ids=["xbf16", "xf16"])
-def test_fused_equals_separate(spec, m, x_dtype, gpu_device):
+def test_fused_equals_separate(spec, m, x_dtype, gpu_device, monkeypatch):
+    # prefill rows (m = 40: 80 rows) on the fused kernel unsplit, whose per-row
+    # arithmetic does not depend on the other linears of the launch
+    monkeypatch.setenv("WAL2026_PREFILL_TWO_PASS", "0")
+    monkeypatch.setenv("WAL2026_PREFILL_KSPLIT", "1")
     mods = _linears(spec, gpu_device, bias=(m == 4))
     fused = FusedBlockRVQLinears(mods)
     x = torch.randn(2, m, spec[2], generator=torch.Generator().manual_seed(m)).to(x_dtype).to(gpu_device)

@@ -757,9 +757,11 @@ class _SiblingFusion:
     same tensor (same object, unchanged since: its version counter, and the
     same stage caps), return theirs from that launch instead of launching
     again.  A call on any other input launches afresh.  Each output is what
-    the linear's own forward returns, bit for bit (the same per-row
-    arithmetic); for several rows of x they are column slices of one buffer,
-    as torch.split returns them.
+    the linear's own forward returns: bit for bit on the decode and unsplit
+    fused prefill kernels (the same per-row arithmetic), to the last bits
+    where the operator takes the two-pass form (the library GEMM of the
+    concatenated weight may sum in another order).  For several rows of x
+    they are column slices of one buffer, as torch.split returns them.
     """
 
     def __init__(self, linears) -> None:
